@@ -1,0 +1,194 @@
+/*
+ * stagehand_native.h — C ABI of the MI355X weight-streaming data path.
+ *
+ * Every entry point returns an int status (SH_OK on success). On failure the
+ * calling thread's last-error string (sh_last_error) names the call and the
+ * cause. No torch types cross this boundary: device buffers are raw device
+ * pointers owned by the caller (PyTorch tensors in the Python layer), streams
+ * and events are opaque handles (hipStream_t / hipEvent_t values; a torch
+ * stream's `cuda_stream` integer may be passed as a stream handle).
+ *
+ * Status → Python exception mapping used by the binding (stagehand_amd/_native.py):
+ *   SH_ERR_INVALID   → ValueError          (reference: PyValueError, turbo_src/lib.rs:59-61;
+ *                                           VmmError::InvalidSlab/InvalidRegion, vmm_src/error.rs:30-53)
+ *   SH_ERR_HIP       → RuntimeError        (reference: "CUDA error {code}", turbo_src/cuda_ffi.rs:62-69)
+ *   SH_ERR_OOM       → StagehandOOMError   (reference: pool capacity, src/stagehand/pool.py:133-139)
+ *   SH_ERR_WATERMARK → MemoryError         (reference: VmmError::Watermarked/NoEvictableRegions)
+ *   SH_ERR_STATE     → RuntimeError        (reference: "No free GPU slots", turbo_src/engine.rs:189)
+ *   SH_ERR_NOT_READY → not an error: the queried event/transfer is still pending
+ *   SH_ERR_TIMEOUT   → TimeoutError
+ */
+#ifndef STAGEHAND_NATIVE_H
+#define STAGEHAND_NATIVE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SH_ABI_VERSION 1
+
+enum sh_status {
+  SH_OK = 0,
+  SH_ERR_INVALID = 1,
+  SH_ERR_HIP = 2,
+  SH_ERR_OOM = 3,
+  SH_ERR_NOT_READY = 4,
+  SH_ERR_STATE = 5,
+  SH_ERR_TIMEOUT = 6,
+  SH_ERR_WATERMARK = 7
+};
+
+/* Thread-local description of the last failure on the calling thread. */
+const char* sh_last_error(void);
+/* SH_ABI_VERSION of the loaded library. */
+int sh_abi_version(void);
+
+/* ───────────────────────── device, streams, events, copies ─────────────────────────
+ * HIP rewrite of the CUDA runtime FFI the reference declares by hand in
+ * turbo_src/cuda_ffi.rs:26-59 (cudaSetDevice, cudaStreamCreateWithFlags,
+ * cudaEventCreateWithFlags/Record/Query/Synchronize, cudaStreamWaitEvent,
+ * cudaMemcpyAsync, cudaMallocHost/cudaFreeHost). */
+
+int sh_device_count(int* count);
+int sh_set_device(int device);                     /* cudaSetDevice, turbo_src/cuda_ffi.rs:57 */
+int sh_get_device(int* device);
+
+/* Pinned host memory (hipHostMalloc, coherent default flags).
+ * Replaces cudaMallocHost/cudaFreeHost, turbo_src/cuda_ffi.rs:29-30. */
+int sh_host_alloc(size_t bytes, void** out);
+int sh_host_free(void* ptr);
+
+/* Non-blocking stream at the default priority.
+ * Replaces cudaStreamCreateWithFlags(.., 1), turbo_src/cuda_ffi.rs:44 and the
+ * torch.cuda.Stream of src/stagehand/transfer.py:95-98. */
+int sh_stream_create(void** out);
+int sh_stream_destroy(void* stream);
+int sh_stream_sync(void* stream);                  /* cudaStreamSynchronize, turbo_src/cuda_ffi.rs:45 */
+int sh_stream_wait_event(void* stream, void* event); /* cudaStreamWaitEvent, turbo_src/cuda_ffi.rs:54 */
+
+/* timing != 0 creates a timing event (for sh_event_elapsed_ms); otherwise
+ * hipEventDisableTiming as in turbo_src/cuda_ffi.rs:49 + EVENT_DISABLE_TIMING. */
+int sh_event_create(int timing, void** out);
+int sh_event_destroy(void* event);
+int sh_event_record(void* event, void* stream);    /* cudaEventRecord, turbo_src/cuda_ffi.rs:50 */
+int sh_event_query(void* event);                   /* SH_OK when complete, SH_ERR_NOT_READY when pending */
+int sh_event_sync(void* event);                    /* cudaEventSynchronize, turbo_src/cuda_ffi.rs:51 */
+int sh_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* Async copies on `stream` (cudaMemcpyAsync kinds 1/2, turbo_src/cuda_ffi.rs:35-41). */
+int sh_memcpy_h2d_async(void* dst_dev, const void* src_host, size_t bytes, void* stream);
+int sh_memcpy_d2h_async(void* dst_host, const void* src_dev, size_t bytes, void* stream);
+int sh_memcpy_d2d_async(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
+
+/* ───────────────────────── slab unpack (dequant / cast) ─────────────────────────
+ * A plan describes how one packed source slab (already in device memory) is
+ * scattered into one destination buffer (a block's contiguous parameter
+ * buffer laid out as in src/stagehand/scheduler.py:148-165: params in
+ * named_parameters() order, offset = running sum of numel * itemsize, no padding).
+ *
+ * One descriptor per parameter region:
+ *   SH_KIND_I8_ROWSCALE_BF16  dst[r*cols+c] = bf16_rne((f32(q[r*src_ld+c]) - zp[r]) * scale[r])
+ *                             the SquareQ dequant of src/stagehand/scheduler.py:290-300
+ *                             (q2d = qweight.reshape(rows,-1)[:out,:in]; src_ld = padded_in).
+ *                             zp is optional (NULL zero_points ⇒ the subtraction is skipped,
+ *                             which is bit-identical to subtracting 0.0f).
+ *   SH_KIND_I8_ROWSCALE_F32   same, fp32 output (runtime dtype float32).
+ *   SH_KIND_F32_BF16          dst[i] = bf16_rne(src_f32[i]); the fp32→bf16 casts of
+ *                             src/stagehand/scheduler.py:181, 224-230, 305, 1071.
+ *   SH_KIND_BF16_F32          dst[i] = f32(src_bf16[i]) (exact widening).
+ *   SH_KIND_COPY_BYTES        dst[i] = src[i] for cols bytes (same-dtype sources: bf16→bf16).
+ *   SH_KIND_ZERO_BYTES        dst[i] = 0 for cols bytes (the zero-fill fallbacks of
+ *                             src/stagehand/scheduler.py:240, 276-297, 325).
+ * bf16_rne is round-to-nearest-even of the fp32 bit pattern; every NaN maps to
+ * 0xFFFF, which is what torch's CPU float→bfloat16 conversion produces.
+ *
+ * rows/cols/src_ld are in elements of the source kind (bytes for the *_BYTES
+ * kinds, where rows must be 1). scale_off indexes `scales` / `zero_points`.
+ * Fields after scale_off are filled in by sh_plan_create and ignored on input.
+ */
+enum sh_kind {
+  SH_KIND_I8_ROWSCALE_BF16 = 1,
+  SH_KIND_I8_ROWSCALE_F32 = 2,
+  SH_KIND_F32_BF16 = 3,
+  SH_KIND_BF16_F32 = 4,
+  SH_KIND_COPY_BYTES = 5,
+  SH_KIND_ZERO_BYTES = 6
+};
+
+typedef struct sh_unpack_desc {
+  uint64_t src_off;    /* byte offset of source element (0,0) in the source buffer */
+  uint64_t dst_off;    /* byte offset of destination element 0 in the destination buffer */
+  uint32_t rows;       /* rows (output features); 1 for flat regions */
+  uint32_t cols;       /* elements per row that are written */
+  uint32_t src_ld;     /* source row stride in elements (>= cols); 0 means cols */
+  uint32_t kind;       /* enum sh_kind */
+  uint64_t scale_off;  /* index of row 0's scale / zero point */
+  /* filled by sh_plan_create: */
+  uint64_t div_magic;  /* ceil(2^64 / cols), 0 when cols == 1 */
+  uint32_t tile_begin; /* first tile of this descriptor */
+  uint32_t ntiles;     /* tiles covering rows*cols elements */
+  uint32_t flags;      /* reserved, 0 */
+  uint32_t reserved;
+} sh_unpack_desc;     /* 64 bytes, identical layout on host and device */
+
+typedef struct sh_plan sh_plan;
+
+typedef struct sh_plan_info {
+  uint32_t n_desc;          /* descriptors after splitting oversize regions */
+  uint32_t n_tiles;         /* workgroups per launch */
+  uint32_t kind_mask;       /* bit (1 << kind) for every kind present */
+  uint32_t tile_elems;      /* elements per tile */
+  uint64_t src_extent;      /* bytes of source the plan reads (max src end) */
+  uint64_t dst_extent;      /* bytes of destination the plan writes (max dst end) */
+  uint64_t scale_extent;    /* scale / zero-point entries the plan reads */
+  uint64_t algo_bytes;      /* algorithmic HBM bytes per launch (reads + writes) */
+  uint64_t elements;        /* elements written */
+} sh_plan_info;
+
+/* Validates the descriptors, splits regions above 2^31 elements by rows, and
+ * uploads the descriptor table and tile map to the current device (the only
+ * device allocation of the unpack path; done once per block layout). */
+int sh_plan_create(const sh_unpack_desc* descs, uint32_t n, sh_plan** out);
+int sh_plan_destroy(sh_plan* plan);
+/* Host-only validation of a descriptor table: fills `info` exactly as
+ * sh_plan_create would, without touching a device. */
+int sh_plan_describe(const sh_unpack_desc* descs, uint32_t n, sh_plan_info* info);
+int sh_plan_get_info(const sh_plan* plan, sh_plan_info* info);
+
+/* Generic launch: one kernel over every descriptor of the plan, on `stream`.
+ * The byte/entry sizes of the buffers are checked against the plan's extents
+ * before anything is launched. scales/zero_points may be NULL when the plan has
+ * no I8 descriptor; zero_points may always be NULL. */
+int sh_unpack(const sh_plan* plan,
+              const void* src, size_t src_bytes,
+              const float* scales, const float* zero_points, size_t n_scale,
+              void* dst, size_t dst_bytes, void* stream);
+
+/* SquareQ INT8→bf16 dequant. Replaces the host dequant of
+ * src/stagehand/scheduler.py:243-325 (core expression :299-300). The plan must
+ * hold only SH_KIND_I8_ROWSCALE_BF16 descriptors. */
+int sh_dequant_i8_rowscale_bf16(const sh_plan* plan,
+                                const int8_t* src, size_t src_bytes,
+                                const float* scales, const float* zero_points, size_t n_scale,
+                                uint16_t* dst, size_t dst_bytes, void* stream);
+
+/* fp32→bf16 slab unpack/cast. Replaces the host casts of
+ * src/stagehand/scheduler.py:168-181 and :1066-1071. The plan must hold only
+ * SH_KIND_F32_BF16 descriptors. */
+int sh_unpack_cast_f32_bf16(const sh_plan* plan,
+                            const float* src, size_t src_bytes,
+                            uint16_t* dst, size_t dst_bytes, void* stream);
+
+/* Host copy of the kernels' row-index division (floor(n[i] / d) through the
+ * 64-bit multiplicative inverse stored in sh_unpack_desc.div_magic), exported
+ * so the index arithmetic can be checked on a CPU. No reference counterpart. */
+int sh_index_div(uint32_t d, const uint32_t* n, uint32_t* q, size_t count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STAGEHAND_NATIVE_H */

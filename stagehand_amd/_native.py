@@ -1,0 +1,193 @@
+"""ctypes binding of ``libstagehand_native.so`` (C ABI in ``include/stagehand_native.h``).
+
+The library is loaded lazily on first use. A missing library is an error, not
+a fallback: every product path that needs it raises :class:`NativeLibraryError`
+telling how to build it.
+
+Status codes map to the exception types the reference raises for the same
+conditions (turbo_src/lib.rs:38-40 → RuntimeError, turbo_src/lib.rs:59-61 →
+ValueError, src/stagehand/pool.py:133-139 → StagehandOOMError,
+vmm_src/error.rs:30-53 → MemoryError for watermark refusals).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+
+from stagehand_amd.errors import StagehandOOMError
+
+__all__ = [
+    "NativeLibraryError",
+    "lib",
+    "check",
+    "LIB_PATH",
+    "DESC_DTYPE",
+    "PLAN_INFO_DTYPE",
+    "SH_OK",
+    "SH_ERR_NOT_READY",
+    "KIND_I8_ROWSCALE_BF16",
+    "KIND_I8_ROWSCALE_F32",
+    "KIND_F32_BF16",
+    "KIND_BF16_F32",
+    "KIND_COPY_BYTES",
+    "KIND_ZERO_BYTES",
+]
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libstagehand_native.so"
+
+SH_OK = 0
+SH_ERR_INVALID = 1
+SH_ERR_HIP = 2
+SH_ERR_OOM = 3
+SH_ERR_NOT_READY = 4
+SH_ERR_STATE = 5
+SH_ERR_TIMEOUT = 6
+SH_ERR_WATERMARK = 7
+
+KIND_I8_ROWSCALE_BF16 = 1
+KIND_I8_ROWSCALE_F32 = 2
+KIND_F32_BF16 = 3
+KIND_BF16_F32 = 4
+KIND_COPY_BYTES = 5
+KIND_ZERO_BYTES = 6
+
+# Mirror of `struct sh_unpack_desc` (64 bytes, little endian, natural alignment).
+DESC_DTYPE = np.dtype(
+    [
+        ("src_off", "<u8"),
+        ("dst_off", "<u8"),
+        ("rows", "<u4"),
+        ("cols", "<u4"),
+        ("src_ld", "<u4"),
+        ("kind", "<u4"),
+        ("scale_off", "<u8"),
+        ("div_magic", "<u8"),
+        ("tile_begin", "<u4"),
+        ("ntiles", "<u4"),
+        ("flags", "<u4"),
+        ("reserved", "<u4"),
+    ]
+)
+assert DESC_DTYPE.itemsize == 64
+
+# Mirror of `struct sh_plan_info`.
+PLAN_INFO_DTYPE = np.dtype(
+    [
+        ("n_desc", "<u4"),
+        ("n_tiles", "<u4"),
+        ("kind_mask", "<u4"),
+        ("tile_elems", "<u4"),
+        ("src_extent", "<u8"),
+        ("dst_extent", "<u8"),
+        ("scale_extent", "<u8"),
+        ("algo_bytes", "<u8"),
+        ("elements", "<u8"),
+    ]
+)
+
+
+class NativeLibraryError(RuntimeError):
+    """The native library is missing or does not match this package."""
+
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_i32 = ctypes.c_int
+_u32 = ctypes.c_uint32
+
+# name → argtypes; every function returns int status.
+_SIGNATURES: dict[str, list] = {
+    "sh_abi_version": [],
+    "sh_device_count": [ctypes.POINTER(_i32)],
+    "sh_set_device": [_i32],
+    "sh_get_device": [ctypes.POINTER(_i32)],
+    "sh_host_alloc": [_sz, ctypes.POINTER(_vp)],
+    "sh_host_free": [_vp],
+    "sh_stream_create": [ctypes.POINTER(_vp)],
+    "sh_stream_destroy": [_vp],
+    "sh_stream_sync": [_vp],
+    "sh_stream_wait_event": [_vp, _vp],
+    "sh_event_create": [_i32, ctypes.POINTER(_vp)],
+    "sh_event_destroy": [_vp],
+    "sh_event_record": [_vp, _vp],
+    "sh_event_query": [_vp],
+    "sh_event_sync": [_vp],
+    "sh_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(ctypes.c_float)],
+    "sh_memcpy_h2d_async": [_vp, _vp, _sz, _vp],
+    "sh_memcpy_d2h_async": [_vp, _vp, _sz, _vp],
+    "sh_memcpy_d2d_async": [_vp, _vp, _sz, _vp],
+    "sh_plan_create": [_vp, _u32, ctypes.POINTER(_vp)],
+    "sh_plan_destroy": [_vp],
+    "sh_plan_get_info": [_vp, _vp],
+    "sh_plan_describe": [_vp, _u32, _vp],
+    "sh_index_div": [_u32, _vp, _vp, _sz],
+    "sh_unpack": [_vp, _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp],
+    "sh_dequant_i8_rowscale_bf16": [_vp, _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp],
+    "sh_unpack_cast_f32_bf16": [_vp, _vp, _sz, _vp, _sz, _vp],
+}
+
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def exported_symbols() -> list[str]:
+    """Names of every C entry point this binding expects the library to export."""
+    return sorted(_SIGNATURES) + ["sh_last_error"]
+
+
+def lib() -> ctypes.CDLL:
+    """Return the loaded native library, loading it on first use."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIB_PATH} is not built; run `python -m stagehand_amd.build_native` "
+                "(or __graft_entry__.build()) first"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        handle.sh_last_error.restype = ctypes.c_char_p
+        handle.sh_last_error.argtypes = []
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        got = handle.sh_abi_version()
+        if got != ABI_VERSION:
+            raise NativeLibraryError(f"{LIB_PATH} has ABI version {got}, expected {ABI_VERSION}; rebuild it")
+        _lib = handle
+        return _lib
+
+
+def last_error() -> str:
+    msg = lib().sh_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(status: int, what: str = "") -> int:
+    """Raise the mapped Python exception for a failed native status."""
+    if status == SH_OK or status == SH_ERR_NOT_READY:
+        return status
+    msg = last_error() or f"{what} failed with status {status}"
+    if status == SH_ERR_INVALID:
+        raise ValueError(msg)
+    if status == SH_ERR_OOM:
+        raise StagehandOOMError(msg)
+    if status == SH_ERR_WATERMARK:
+        raise MemoryError(msg)
+    if status == SH_ERR_TIMEOUT:
+        raise TimeoutError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> int:
+    """Call native entry point *name* and raise on failure."""
+    return check(getattr(lib(), name)(*args), name)

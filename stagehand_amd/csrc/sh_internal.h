@@ -1,0 +1,45 @@
+// Internal helpers shared by the native sources: error reporting and the
+// division-by-invariant used to map a flat element index to its row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "stagehand_native.h"
+
+namespace sh {
+
+// Records the failure text for sh_last_error() on the calling thread and
+// returns `status` so call sites can `return fail(...)`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// HIP call wrapper: converts a hipError_t into SH_ERR_HIP with the call text.
+#define SH_HIP(call)                                                              \
+  do {                                                                            \
+    hipError_t sh_e_ = (call);                                                    \
+    if (sh_e_ != hipSuccess)                                                      \
+      return ::sh::fail(SH_ERR_HIP, "HIP error %d (%s) in %s", (int)sh_e_,       \
+                        hipGetErrorString(sh_e_), #call);                         \
+  } while (0)
+
+// floor(n / d) for every 32-bit n, with magic = ceil(2^64 / d) for d >= 2 and
+// magic = 0 for d == 1. The quotient is floor(n * magic / 2^64): with
+// magic = 2^64/d + eps (0 <= eps < 1), the error term n*eps/2^64 < 2^-32 <= 1/d
+// never carries the fractional part of n/d past the next integer.
+__host__ __device__ inline uint64_t udiv_magic(uint32_t d) {
+  return d <= 1 ? 0ull : (UINT64_MAX / d) + 1ull;
+}
+
+__host__ __device__ inline uint32_t udiv(uint32_t n, uint64_t magic) {
+  if (magic == 0) return n;
+  const uint64_t lo = (uint64_t)n * (uint32_t)magic;
+  const uint64_t hi = (uint64_t)n * (uint32_t)(magic >> 32);
+  return (uint32_t)((hi + (lo >> 32)) >> 32);
+}
+
+}  // namespace sh

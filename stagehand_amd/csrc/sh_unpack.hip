@@ -1,0 +1,696 @@
+// Slab unpack kernels for gfx950: SquareQ INT8→bf16 dequant and fp32→bf16
+// cast, scattering a packed device-resident source slab into a block's
+// contiguous parameter buffer.
+//
+// Replaces the host-side staging arithmetic of the reference:
+//   SquareQ dequant   src/stagehand/scheduler.py:290-300
+//   bias / param cast src/stagehand/scheduler.py:181, 224-230, 302-306, 1066-1071
+//   zero-fill         src/stagehand/scheduler.py:240, 276-297, 325
+//
+// Work decomposition. Every descriptor covers rows*cols elements, cut into
+// tiles of kThreads * kChunk * kUnroll elements; a host-built tile map gives
+// each workgroup its descriptor in O(1) (one scalar load), and the descriptor
+// itself is a 64-byte scalar load, so all per-region state lives in SGPRs.
+// Each thread moves kUnroll chunks of 16 elements; all loads of a thread are
+// issued before the first conversion, so a wave keeps 4 x 16 B (int8) or
+// 4 x 64 B (fp32) per lane in flight. Loads and stores are 128-bit; the
+// hardware's unaligned-access mode lets them start at any byte offset, which
+// the reference layout needs (it has no padding, so int8 regions start at
+// arbitrary offsets). This is pure streaming: no LDS and no MFMA.
+//
+// Numerics. The dequant is computed exactly as the reference's torch CPU ops:
+// f32(q) exactly, then an IEEE fp32 subtract of the zero point (skipped when
+// no zero points are given: q - 0.0f == q bit for bit), then an IEEE fp32
+// multiply by the row scale, each rounded to nearest even; fp32 denormals are
+// kept (no flush flags). Contraction is disabled so nothing becomes an FMA.
+// fp32→bf16 is round-to-nearest-even on the bit pattern,
+//   bf16 = (u + 0x7FFF + ((u >> 16) & 1)) >> 16,
+// which equals torch's CPU conversion for every non-NaN input; every NaN
+// becomes 0xFFFF, as torch's CPU conversion does.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "sh_internal.h"
+#include "stagehand_native.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kChunk = 16;  // elements per thread per chunk (16-element kinds)
+constexpr uint32_t kChunkBytes = 64;  // bytes per thread per chunk (byte kinds)
+constexpr uint32_t kUnroll = 4;
+constexpr uint32_t kTileElems = kThreads * kChunk * kUnroll;       // 16384
+constexpr uint32_t kTileBytes = kThreads * kChunkBytes * kUnroll;  // 65536
+constexpr uint64_t kMaxDescElems = 1ull << 31;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+  u32x4 v;
+  __builtin_memcpy(&v, p, 16);
+  return v;
+}
+
+__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_memcpy(p, &v, 16); }
+
+// Rounded bf16 in bits 31..16 (low half is garbage): u + 0x7FFF + lsb.
+__device__ __forceinline__ uint32_t rne_hi(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return u + 0x7FFFu + ((u >> 16) & 1u);
+}
+
+__device__ __forceinline__ uint32_t rne_hi_nan(float x) {
+  return (x != x) ? 0xFFFFFFFFu : rne_hi(x);
+}
+
+// Packs the upper halves of two rne_hi words: lo element in bits 15..0.
+__device__ __forceinline__ uint32_t pack_hi(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(rne_hi_nan(x) >> 16); }
+
+__device__ __forceinline__ float i8_at(uint32_t word, int byte) {
+  return (float)(int32_t)(int8_t)(uint8_t)(word >> (8 * byte));
+}
+
+template <bool HAS_ZP>
+__device__ __forceinline__ float dq(float q, float s, float z) {
+  if (HAS_ZP) q = q - z;
+  return q * s;
+}
+
+// ── INT8 row-scale dequant ────────────────────────────────────────────────
+
+template <bool OUT_BF16, bool HAS_ZP, bool NANCHK>
+__device__ __forceinline__ void dq16_store(u32x4 q, float s, float z, uint8_t* out) {
+  if (OUT_BF16) {
+    u32x4 o0, o1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t word = q[w];
+      const float f0 = dq<HAS_ZP>(i8_at(word, 0), s, z);
+      const float f1 = dq<HAS_ZP>(i8_at(word, 1), s, z);
+      const float f2 = dq<HAS_ZP>(i8_at(word, 2), s, z);
+      const float f3 = dq<HAS_ZP>(i8_at(word, 3), s, z);
+      const uint32_t a = NANCHK ? pack_hi(rne_hi_nan(f0), rne_hi_nan(f1)) : pack_hi(rne_hi(f0), rne_hi(f1));
+      const uint32_t b = NANCHK ? pack_hi(rne_hi_nan(f2), rne_hi_nan(f3)) : pack_hi(rne_hi(f2), rne_hi(f3));
+      if (w < 2) {
+        o0[2 * w] = a;
+        o0[2 * w + 1] = b;
+      } else {
+        o1[2 * (w - 2)] = a;
+        o1[2 * (w - 2) + 1] = b;
+      }
+    }
+    st16(out, o0);
+    st16(out + 16, o1);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t word = q[w];
+      u32x4 o;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) o[b] = __float_as_uint(dq<HAS_ZP>(i8_at(word, b), s, z));
+      st16(out + 16 * w, o);
+    }
+  }
+}
+
+template <bool OUT_BF16>
+__device__ __forceinline__ void store_elem(uint8_t* o, uint32_t idx, float v) {
+  if (OUT_BF16) {
+    const uint16_t b = bf16_bits(v);
+    __builtin_memcpy(o + 2 * (size_t)idx, &b, 2);
+  } else {
+    __builtin_memcpy(o + 4 * (size_t)idx, &v, 4);
+  }
+}
+
+template <bool OUT_BF16, bool HAS_ZP>
+__device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
+                                        const uint8_t* __restrict__ src,
+                                        const float* __restrict__ scales,
+                                        const float* __restrict__ zps, uint8_t* __restrict__ dst) {
+  const uint32_t cols = d.cols;
+  const uint32_t numel = d.rows * cols;
+  const uint32_t ld = d.src_ld ? d.src_ld : cols;
+  const uint8_t* s = src + d.src_off;
+  uint8_t* o = dst + d.dst_off;
+  const float* sc = scales + d.scale_off;
+  const float* zp = HAS_ZP ? zps + d.scale_off : nullptr;
+  constexpr uint32_t kOutBytes = OUT_BF16 ? 2 : 4;
+  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
+
+  if (ld == cols && (cols % kChunk) == 0) {
+    // Every chunk lies inside one row: one scale per 16 elements.
+    u32x4 q[kUnroll];
+    float sv[kUnroll], zv[kUnroll];
+#pragma unroll
+    for (uint32_t k = 0; k < kUnroll; ++k) {
+      const uint32_t e = e0 + k * (kThreads * kChunk);
+      if (e < numel) q[k] = ld16(s + e);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kUnroll; ++k) {
+      const uint32_t e = e0 + k * (kThreads * kChunk);
+      if (e < numel) {
+        const uint32_t r = sh::udiv(e, d.div_magic);
+        sv[k] = sc[r];
+        zv[k] = HAS_ZP ? zp[r] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kUnroll; ++k) {
+      const uint32_t e = e0 + k * (kThreads * kChunk);
+      if (e < numel) {
+        uint8_t* out = o + (size_t)e * kOutBytes;
+        // Finite scale and zero point cannot produce NaN from a finite q.
+        if (__builtin_isfinite(sv[k]) && (!HAS_ZP || __builtin_isfinite(zv[k])))
+          dq16_store<OUT_BF16, HAS_ZP, false>(q[k], sv[k], zv[k], out);
+        else
+          dq16_store<OUT_BF16, HAS_ZP, true>(q[k], sv[k], zv[k], out);
+      }
+    }
+    return;
+  }
+
+  // Rows shorter than or not a multiple of 16, or a padded source (ld > cols):
+  // element-wise with the row tracked incrementally inside each chunk.
+#pragma unroll 1
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t e = e0 + k * (kThreads * kChunk);
+    if (e >= numel) break;
+    uint32_t r = sh::udiv(e, d.div_magic);
+    uint32_t c = e - r * cols;
+    const uint32_t n = min(kChunk, numel - e);
+    if (ld == cols && n == kChunk) {
+      const u32x4 q = ld16(s + e);
+      if (OUT_BF16) {
+        uint32_t hw[kChunk];
+#pragma unroll
+        for (uint32_t j = 0; j < kChunk; ++j) {
+          const float f = dq<HAS_ZP>(i8_at(q[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f);
+          hw[j] = rne_hi_nan(f);
+          if (++c == cols) {
+            c = 0;
+            ++r;
+          }
+        }
+        u32x4 o0, o1;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o0[w] = pack_hi(hw[2 * w], hw[2 * w + 1]);
+          o1[w] = pack_hi(hw[8 + 2 * w], hw[8 + 2 * w + 1]);
+        }
+        st16(o + (size_t)e * 2, o0);
+        st16(o + (size_t)e * 2 + 16, o1);
+      } else {
+#pragma unroll
+        for (uint32_t j = 0; j < kChunk; ++j) {
+          const float f = dq<HAS_ZP>(i8_at(q[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f);
+          store_elem<false>(o, e + j, f);
+          if (++c == cols) {
+            c = 0;
+            ++r;
+          }
+        }
+      }
+    } else {
+      for (uint32_t j = 0; j < n; ++j) {
+        const float q = (float)(int32_t)(int8_t)s[(size_t)r * ld + c];
+        store_elem<OUT_BF16>(o, e + j, dq<HAS_ZP>(q, sc[r], HAS_ZP ? zp[r] : 0.0f));
+        if (++c == cols) {
+          c = 0;
+          ++r;
+        }
+      }
+    }
+  }
+}
+
+// ── fp32 → bf16 cast ──────────────────────────────────────────────────────
+
+__device__ __forceinline__ void tile_f32_bf16(const sh_unpack_desc& d, uint32_t local,
+                                              const uint8_t* __restrict__ src,
+                                              uint8_t* __restrict__ dst) {
+  const uint32_t numel = d.rows * d.cols;
+  const uint8_t* s = src + d.src_off;
+  uint8_t* o = dst + d.dst_off;
+  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
+  u32x4 v[kUnroll][4];
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t e = e0 + k * (kThreads * kChunk);
+    if (e + kChunk <= numel) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[k][i] = ld16(s + (size_t)e * 4 + 16 * i);
+    }
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t e = e0 + k * (kThreads * kChunk);
+    if (e + kChunk <= numel) {
+      u32x4 o0, o1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        o0[2 * i] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i][0])), rne_hi_nan(__uint_as_float(v[k][i][1])));
+        o0[2 * i + 1] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i][2])), rne_hi_nan(__uint_as_float(v[k][i][3])));
+        o1[2 * i] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i + 2][0])), rne_hi_nan(__uint_as_float(v[k][i + 2][1])));
+        o1[2 * i + 1] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i + 2][2])), rne_hi_nan(__uint_as_float(v[k][i + 2][3])));
+      }
+      st16(o + (size_t)e * 2, o0);
+      st16(o + (size_t)e * 2 + 16, o1);
+    } else if (e < numel) {
+      for (uint32_t j = e; j < numel; ++j) {
+        float x;
+        __builtin_memcpy(&x, s + (size_t)j * 4, 4);
+        const uint16_t b = bf16_bits(x);
+        __builtin_memcpy(o + (size_t)j * 2, &b, 2);
+      }
+    }
+  }
+}
+
+// ── bf16 → fp32 widen ─────────────────────────────────────────────────────
+
+__device__ __forceinline__ void tile_bf16_f32(const sh_unpack_desc& d, uint32_t local,
+                                              const uint8_t* __restrict__ src,
+                                              uint8_t* __restrict__ dst) {
+  const uint32_t numel = d.rows * d.cols;
+  const uint8_t* s = src + d.src_off;
+  uint8_t* o = dst + d.dst_off;
+  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
+  u32x4 v[kUnroll][2];
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t e = e0 + k * (kThreads * kChunk);
+    if (e + kChunk <= numel) {
+      v[k][0] = ld16(s + (size_t)e * 2);
+      v[k][1] = ld16(s + (size_t)e * 2 + 16);
+    }
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t e = e0 + k * (kThreads * kChunk);
+    if (e + kChunk <= numel) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          u32x4 w;
+          w[0] = v[k][h][2 * p] << 16;
+          w[1] = v[k][h][2 * p] & 0xFFFF0000u;
+          w[2] = v[k][h][2 * p + 1] << 16;
+          w[3] = v[k][h][2 * p + 1] & 0xFFFF0000u;
+          st16(o + (size_t)e * 4 + 32 * h + 16 * p, w);
+        }
+      }
+    } else if (e < numel) {
+      for (uint32_t j = e; j < numel; ++j) {
+        uint16_t b;
+        __builtin_memcpy(&b, s + (size_t)j * 2, 2);
+        const uint32_t w = (uint32_t)b << 16;
+        __builtin_memcpy(o + (size_t)j * 4, &w, 4);
+      }
+    }
+  }
+}
+
+// ── byte copy / zero fill ─────────────────────────────────────────────────
+
+template <bool ZERO>
+__device__ __forceinline__ void tile_bytes(const sh_unpack_desc& d, uint32_t local,
+                                           const uint8_t* __restrict__ src,
+                                           uint8_t* __restrict__ dst) {
+  const uint32_t nbytes = d.rows * d.cols;
+  const uint8_t* s = src + d.src_off;
+  uint8_t* o = dst + d.dst_off;
+  const uint32_t b0 = local * kTileBytes + threadIdx.x * kChunkBytes;
+  u32x4 v[kUnroll][4];
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t b = b0 + k * (kThreads * kChunkBytes);
+    if (b + kChunkBytes <= nbytes) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[k][i] = ZERO ? u32x4{0, 0, 0, 0} : ld16(s + b + 16 * i);
+    }
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kUnroll; ++k) {
+    const uint32_t b = b0 + k * (kThreads * kChunkBytes);
+    if (b + kChunkBytes <= nbytes) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st16(o + b + 16 * i, v[k][i]);
+    } else if (b < nbytes) {
+      for (uint32_t j = b; j < nbytes; ++j) o[j] = ZERO ? (uint8_t)0 : s[j];
+    }
+  }
+}
+
+// ── kernels ───────────────────────────────────────────────────────────────
+
+constexpr uint32_t bit(uint32_t kind) { return 1u << kind; }
+constexpr uint32_t kMaskDequantBf16 = bit(SH_KIND_I8_ROWSCALE_BF16);
+constexpr uint32_t kMaskCastBf16 = bit(SH_KIND_F32_BF16);
+constexpr uint32_t kMaskAll = bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROWSCALE_F32) |
+                              bit(SH_KIND_F32_BF16) | bit(SH_KIND_BF16_F32) |
+                              bit(SH_KIND_COPY_BYTES) | bit(SH_KIND_ZERO_BYTES);
+
+template <uint32_t MASK, bool HAS_ZP>
+__device__ __forceinline__ void unpack_body(const sh_unpack_desc* __restrict__ descs,
+                                            const uint32_t* __restrict__ tile_map,
+                                            const uint8_t* __restrict__ src,
+                                            const float* __restrict__ scales,
+                                            const float* __restrict__ zps,
+                                            uint8_t* __restrict__ dst) {
+  const uint32_t tile = blockIdx.x;
+  const sh_unpack_desc d = descs[tile_map[tile]];
+  const uint32_t local = tile - d.tile_begin;
+  switch (d.kind) {
+    case SH_KIND_I8_ROWSCALE_BF16:
+      if constexpr ((MASK & bit(SH_KIND_I8_ROWSCALE_BF16)) != 0)
+        tile_i8<true, HAS_ZP>(d, local, src, scales, zps, dst);
+      break;
+    case SH_KIND_I8_ROWSCALE_F32:
+      if constexpr ((MASK & bit(SH_KIND_I8_ROWSCALE_F32)) != 0)
+        tile_i8<false, HAS_ZP>(d, local, src, scales, zps, dst);
+      break;
+    case SH_KIND_F32_BF16:
+      if constexpr ((MASK & bit(SH_KIND_F32_BF16)) != 0) tile_f32_bf16(d, local, src, dst);
+      break;
+    case SH_KIND_BF16_F32:
+      if constexpr ((MASK & bit(SH_KIND_BF16_F32)) != 0) tile_bf16_f32(d, local, src, dst);
+      break;
+    case SH_KIND_COPY_BYTES:
+      if constexpr ((MASK & bit(SH_KIND_COPY_BYTES)) != 0) tile_bytes<false>(d, local, src, dst);
+      break;
+    case SH_KIND_ZERO_BYTES:
+      if constexpr ((MASK & bit(SH_KIND_ZERO_BYTES)) != 0) tile_bytes<true>(d, local, src, dst);
+      break;
+    default:
+      break;
+  }
+}
+
+}  // namespace
+
+#define SH_KERNEL_ARGS                                                                 \
+  const sh_unpack_desc *__restrict__ descs, const uint32_t *__restrict__ tile_map,    \
+      const uint8_t *__restrict__ src, const float *__restrict__ scales,              \
+      const float *__restrict__ zps, uint8_t *__restrict__ dst
+
+extern "C" __global__ __launch_bounds__(kThreads) void sh_dequant_i8_bf16_kernel(SH_KERNEL_ARGS) {
+  unpack_body<kMaskDequantBf16, false>(descs, tile_map, src, scales, zps, dst);
+}
+extern "C" __global__ __launch_bounds__(kThreads) void sh_dequant_i8_bf16_zp_kernel(SH_KERNEL_ARGS) {
+  unpack_body<kMaskDequantBf16, true>(descs, tile_map, src, scales, zps, dst);
+}
+extern "C" __global__ __launch_bounds__(kThreads) void sh_cast_f32_bf16_kernel(SH_KERNEL_ARGS) {
+  unpack_body<kMaskCastBf16, false>(descs, tile_map, src, scales, zps, dst);
+}
+extern "C" __global__ __launch_bounds__(kThreads) void sh_unpack_mixed_kernel(SH_KERNEL_ARGS) {
+  unpack_body<kMaskAll, false>(descs, tile_map, src, scales, zps, dst);
+}
+extern "C" __global__ __launch_bounds__(kThreads) void sh_unpack_mixed_zp_kernel(SH_KERNEL_ARGS) {
+  unpack_body<kMaskAll, true>(descs, tile_map, src, scales, zps, dst);
+}
+
+namespace {
+
+// ── host side: plans ──────────────────────────────────────────────────────
+
+bool is_i8(uint32_t kind) {
+  return kind == SH_KIND_I8_ROWSCALE_BF16 || kind == SH_KIND_I8_ROWSCALE_F32;
+}
+bool is_bytes(uint32_t kind) { return kind == SH_KIND_COPY_BYTES || kind == SH_KIND_ZERO_BYTES; }
+uint32_t src_elem_bytes(uint32_t kind) {
+  switch (kind) {
+    case SH_KIND_I8_ROWSCALE_BF16:
+    case SH_KIND_I8_ROWSCALE_F32:
+    case SH_KIND_COPY_BYTES: return 1;
+    case SH_KIND_F32_BF16: return 4;
+    case SH_KIND_BF16_F32: return 2;
+    default: return 0;  // ZERO reads nothing
+  }
+}
+uint32_t dst_elem_bytes(uint32_t kind) {
+  switch (kind) {
+    case SH_KIND_I8_ROWSCALE_BF16:
+    case SH_KIND_F32_BF16: return 2;
+    case SH_KIND_I8_ROWSCALE_F32:
+    case SH_KIND_BF16_F32: return 4;
+    default: return 1;
+  }
+}
+
+}  // namespace
+
+struct sh_plan {
+  int device = -1;
+  std::vector<sh_unpack_desc> host;
+  sh_unpack_desc* d_descs = nullptr;
+  uint32_t* d_tile_map = nullptr;
+  sh_plan_info info{};
+};
+
+namespace {
+
+// Validates the caller's descriptors and produces the launch table (oversize
+// regions split, tiles assigned) and its summary. Host only: no device calls.
+int build_table(const sh_unpack_desc* descs, uint32_t n, std::vector<sh_unpack_desc>& table,
+                sh_plan_info& info, const char* who) {
+  if (n > 0 && descs == nullptr) return sh::fail(SH_ERR_INVALID, "%s: descs is NULL", who);
+  table.clear();
+  table.reserve(n);
+  info = sh_plan_info{};
+  info.tile_elems = kTileElems;
+  uint64_t tiles = 0;
+
+  auto push = [&](sh_unpack_desc d) -> int {
+    const uint64_t numel = (uint64_t)d.rows * d.cols;
+    d.div_magic = sh::udiv_magic(d.cols);
+    const uint64_t per_tile = is_bytes(d.kind) ? kTileBytes : kTileElems;
+    const uint64_t nt = (numel + per_tile - 1) / per_tile;
+    if (tiles + nt > 0x7FFFFFFFull)
+      return sh::fail(SH_ERR_INVALID, "%s: plan needs more than 2^31-1 tiles", who);
+    d.tile_begin = (uint32_t)tiles;
+    d.ntiles = (uint32_t)nt;
+    d.flags = 0;
+    d.reserved = 0;
+    tiles += nt;
+    const uint32_t ld = d.src_ld ? d.src_ld : d.cols;
+    const uint64_t src_span =
+        is_i8(d.kind) ? ((uint64_t)(d.rows - 1) * ld + d.cols) : numel * src_elem_bytes(d.kind);
+    if (d.kind != SH_KIND_ZERO_BYTES) info.src_extent = std::max(info.src_extent, d.src_off + src_span);
+    info.dst_extent = std::max(info.dst_extent, d.dst_off + numel * dst_elem_bytes(d.kind));
+    if (is_i8(d.kind)) {
+      info.scale_extent = std::max(info.scale_extent, d.scale_off + d.rows);
+      info.algo_bytes += 4ull * d.rows;
+    }
+    info.algo_bytes += numel * (src_elem_bytes(d.kind) + dst_elem_bytes(d.kind));
+    info.elements += numel;
+    info.kind_mask |= bit(d.kind);
+    table.push_back(d);
+    return SH_OK;
+  };
+
+  for (uint32_t i = 0; i < n; ++i) {
+    sh_unpack_desc d = descs[i];
+    if (d.kind < SH_KIND_I8_ROWSCALE_BF16 || d.kind > SH_KIND_ZERO_BYTES)
+      return sh::fail(SH_ERR_INVALID, "%s: descriptor %u has unknown kind %u", who, i, d.kind);
+    if (d.rows == 0 || d.cols == 0) continue;  // empty region: nothing to write
+    const uint32_t ld = d.src_ld ? d.src_ld : d.cols;
+    if (is_i8(d.kind)) {
+      if (ld < d.cols)
+        return sh::fail(SH_ERR_INVALID, "%s: descriptor %u has src_ld %u < cols %u", who, i, ld, d.cols);
+      if (d.cols > kMaxDescElems)
+        return sh::fail(SH_ERR_INVALID, "%s: descriptor %u row of %u elements is too long", who, i, d.cols);
+      d.src_ld = ld;
+      // Split by rows so every piece holds at most 2^31 elements (32-bit indexing in the kernel).
+      const uint32_t rows_per = (uint32_t)std::min<uint64_t>(d.rows, kMaxDescElems / d.cols);
+      for (uint32_t r0 = 0; r0 < d.rows; r0 += rows_per) {
+        sh_unpack_desc p = d;
+        p.rows = std::min(rows_per, d.rows - r0);
+        p.src_off = d.src_off + (uint64_t)r0 * ld;
+        p.dst_off = d.dst_off + (uint64_t)r0 * d.cols * dst_elem_bytes(d.kind);
+        p.scale_off = d.scale_off + r0;
+        if (int st = push(p)) return st;
+      }
+    } else {
+      if (ld != d.cols)
+        return sh::fail(SH_ERR_INVALID, "%s: descriptor %u of kind %u must be contiguous (src_ld == cols)", who, i, d.kind);
+      // Flat region: re-cut into rows of at most 2^30 elements.
+      uint64_t numel = (uint64_t)d.rows * d.cols;
+      uint64_t done = 0;
+      while (done < numel) {
+        const uint64_t piece = std::min<uint64_t>(numel - done, 1ull << 30);
+        sh_unpack_desc p = d;
+        p.rows = 1;
+        p.cols = (uint32_t)piece;
+        p.src_ld = (uint32_t)piece;
+        p.src_off = d.src_off + done * src_elem_bytes(d.kind);
+        p.dst_off = d.dst_off + done * dst_elem_bytes(d.kind);
+        if (int st = push(p)) return st;
+        done += piece;
+      }
+    }
+  }
+  info.n_desc = (uint32_t)table.size();
+  info.n_tiles = (uint32_t)tiles;
+  return SH_OK;
+}
+
+}  // namespace
+
+extern "C" int sh_plan_describe(const sh_unpack_desc* descs, uint32_t n, sh_plan_info* info) {
+  sh::clear_error();
+  if (info == nullptr) return sh::fail(SH_ERR_INVALID, "sh_plan_describe: info is NULL");
+  std::vector<sh_unpack_desc> table;
+  return build_table(descs, n, table, *info, "sh_plan_describe");
+}
+
+extern "C" int sh_plan_create(const sh_unpack_desc* descs, uint32_t n, sh_plan** out) {
+  sh::clear_error();
+  if (out == nullptr) return sh::fail(SH_ERR_INVALID, "sh_plan_create: out is NULL");
+  *out = nullptr;
+  std::vector<sh_unpack_desc> table;
+  sh_plan_info info{};
+  if (int st = build_table(descs, n, table, info, "sh_plan_create")) return st;
+  const uint64_t tiles = info.n_tiles;
+
+  sh_plan* plan = new (std::nothrow) sh_plan();
+  if (plan == nullptr) return sh::fail(SH_ERR_OOM, "sh_plan_create: out of host memory");
+  plan->host = std::move(table);
+  plan->info = info;
+  hipError_t e = hipGetDevice(&plan->device);
+  if (e != hipSuccess) {
+    delete plan;
+    return sh::fail(SH_ERR_HIP, "HIP error %d (%s) in hipGetDevice", (int)e, hipGetErrorString(e));
+  }
+  if (!plan->host.empty()) {
+    std::vector<uint32_t> tile_map(tiles);
+    for (uint32_t i = 0; i < plan->host.size(); ++i) {
+      const sh_unpack_desc& d = plan->host[i];
+      std::fill(tile_map.begin() + d.tile_begin, tile_map.begin() + d.tile_begin + d.ntiles, i);
+    }
+    const size_t desc_bytes = plan->host.size() * sizeof(sh_unpack_desc);
+    const size_t map_bytes = tile_map.size() * sizeof(uint32_t);
+    e = hipMalloc((void**)&plan->d_descs, desc_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&plan->d_tile_map, map_bytes);
+    if (e == hipSuccess) e = hipMemcpy(plan->d_descs, plan->host.data(), desc_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(plan->d_tile_map, tile_map.data(), map_bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(plan->d_descs);
+      (void)hipFree(plan->d_tile_map);
+      delete plan;
+      return sh::fail(e == hipErrorOutOfMemory ? SH_ERR_OOM : SH_ERR_HIP,
+                      "HIP error %d (%s) uploading an unpack plan", (int)e, hipGetErrorString(e));
+    }
+  }
+  *out = plan;
+  return SH_OK;
+}
+
+extern "C" int sh_plan_destroy(sh_plan* plan) {
+  sh::clear_error();
+  if (plan == nullptr) return SH_OK;
+  int cur = -1;
+  (void)hipGetDevice(&cur);
+  if (plan->device >= 0 && cur != plan->device) (void)hipSetDevice(plan->device);
+  hipError_t e1 = plan->d_descs ? hipFree(plan->d_descs) : hipSuccess;
+  hipError_t e2 = plan->d_tile_map ? hipFree(plan->d_tile_map) : hipSuccess;
+  if (plan->device >= 0 && cur >= 0 && cur != plan->device) (void)hipSetDevice(cur);
+  delete plan;
+  if (e1 != hipSuccess || e2 != hipSuccess)
+    return sh::fail(SH_ERR_HIP, "HIP error %d freeing an unpack plan", (int)(e1 != hipSuccess ? e1 : e2));
+  return SH_OK;
+}
+
+extern "C" int sh_plan_get_info(const sh_plan* plan, sh_plan_info* info) {
+  sh::clear_error();
+  if (plan == nullptr || info == nullptr) return sh::fail(SH_ERR_INVALID, "sh_plan_get_info: NULL argument");
+  *info = plan->info;
+  return SH_OK;
+}
+
+namespace {
+
+int launch(const sh_plan* plan, const void* src, size_t src_bytes, const float* scales,
+           const float* zps, size_t n_scale, void* dst, size_t dst_bytes, void* stream,
+           uint32_t required_mask, const char* who) {
+  sh::clear_error();
+  if (plan == nullptr) return sh::fail(SH_ERR_INVALID, "%s: plan is NULL", who);
+  const sh_plan_info& in = plan->info;
+  if (required_mask != 0 && (in.kind_mask & ~required_mask) != 0)
+    return sh::fail(SH_ERR_INVALID, "%s: plan holds descriptor kinds (mask 0x%x) this entry point does not handle",
+                    who, in.kind_mask);
+  if (in.n_tiles == 0) return SH_OK;
+  int cur = -1;
+  SH_HIP(hipGetDevice(&cur));
+  if (cur != plan->device)
+    return sh::fail(SH_ERR_INVALID, "%s: plan was built on device %d but device %d is current", who,
+                    plan->device, cur);
+  if (in.src_extent > 0 && (src == nullptr || src_bytes < in.src_extent))
+    return sh::fail(SH_ERR_INVALID, "%s: source buffer of %zu bytes is smaller than the plan's %llu", who,
+                    src == nullptr ? (size_t)0 : src_bytes, (unsigned long long)in.src_extent);
+  if (dst == nullptr || dst_bytes < in.dst_extent)
+    return sh::fail(SH_ERR_INVALID, "%s: destination buffer of %zu bytes is smaller than the plan's %llu", who,
+                    dst == nullptr ? (size_t)0 : dst_bytes, (unsigned long long)in.dst_extent);
+  const bool has_i8 = (in.kind_mask & (bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROWSCALE_F32))) != 0;
+  if (has_i8 && (scales == nullptr || n_scale < in.scale_extent))
+    return sh::fail(SH_ERR_INVALID, "%s: %zu scales given, the plan reads %llu", who,
+                    scales == nullptr ? (size_t)0 : n_scale, (unsigned long long)in.scale_extent);
+  const bool has_zp = has_i8 && zps != nullptr;
+
+  void (*kern)(SH_KERNEL_ARGS);
+  if (in.kind_mask == kMaskDequantBf16)
+    kern = has_zp ? sh_dequant_i8_bf16_zp_kernel : sh_dequant_i8_bf16_kernel;
+  else if (in.kind_mask == kMaskCastBf16)
+    kern = sh_cast_f32_bf16_kernel;
+  else
+    kern = has_zp ? sh_unpack_mixed_zp_kernel : sh_unpack_mixed_kernel;
+
+  hipLaunchKernelGGL(kern, dim3(in.n_tiles), dim3(kThreads), 0, (hipStream_t)stream, plan->d_descs,
+                     plan->d_tile_map, (const uint8_t*)src, scales, has_zp ? zps : nullptr, (uint8_t*)dst);
+  SH_HIP(hipGetLastError());
+  return SH_OK;
+}
+
+}  // namespace
+
+extern "C" int sh_unpack(const sh_plan* plan, const void* src, size_t src_bytes, const float* scales,
+                         const float* zero_points, size_t n_scale, void* dst, size_t dst_bytes,
+                         void* stream) {
+  return launch(plan, src, src_bytes, scales, zero_points, n_scale, dst, dst_bytes, stream, 0, "sh_unpack");
+}
+
+extern "C" int sh_dequant_i8_rowscale_bf16(const sh_plan* plan, const int8_t* src, size_t src_bytes,
+                                           const float* scales, const float* zero_points, size_t n_scale,
+                                           uint16_t* dst, size_t dst_bytes, void* stream) {
+  return launch(plan, src, src_bytes, scales, zero_points, n_scale, dst, dst_bytes, stream, kMaskDequantBf16,
+                "sh_dequant_i8_rowscale_bf16");
+}
+
+extern "C" int sh_unpack_cast_f32_bf16(const sh_plan* plan, const float* src, size_t src_bytes, uint16_t* dst,
+                                       size_t dst_bytes, void* stream) {
+  return launch(plan, src, src_bytes, nullptr, nullptr, 0, dst, dst_bytes, stream, kMaskCastBf16,
+                "sh_unpack_cast_f32_bf16");
+}
+
+extern "C" int sh_index_div(uint32_t d, const uint32_t* n, uint32_t* q, size_t count) {
+  sh::clear_error();
+  if (d == 0) return sh::fail(SH_ERR_INVALID, "sh_index_div: divisor is 0");
+  if (count > 0 && (n == nullptr || q == nullptr)) return sh::fail(SH_ERR_INVALID, "sh_index_div: NULL array");
+  const uint64_t m = sh::udiv_magic(d);
+  for (size_t i = 0; i < count; ++i) q[i] = sh::udiv(n[i], m);
+  return SH_OK;
+}

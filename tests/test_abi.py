@@ -1,0 +1,143 @@
+"""The C ABI library loads, exports every declared entry point, and its
+host-only logic (plan validation, row-index division) is correct. No call
+here touches a GPU."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from stagehand_amd import _native
+from stagehand_amd._native import DESC_DTYPE, PLAN_INFO_DTYPE
+from stagehand_amd.unpack import (
+    KIND_BF16_F32,
+    KIND_COPY_BYTES,
+    KIND_F32_BF16,
+    KIND_I8_ROWSCALE_BF16,
+    KIND_I8_ROWSCALE_F32,
+    KIND_ZERO_BYTES,
+    make_descs,
+)
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "stagehand_native.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(sh_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    names = declared_functions()
+    assert len(names) >= 25
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.exported_symbols())
+
+
+def test_abi_version_and_last_error():
+    lib = _native.lib()
+    assert lib.sh_abi_version() == _native.ABI_VERSION
+    st = lib.sh_plan_describe(None, 1, None)
+    assert st == _native.SH_ERR_INVALID
+    assert "info is NULL" in _native.last_error()
+
+
+def test_struct_sizes_match_header():
+    assert DESC_DTYPE.itemsize == 64
+    assert PLAN_INFO_DTYPE.itemsize == 56
+
+
+def describe(rows) -> dict:
+    table = make_descs(rows)
+    info = np.zeros(1, dtype=PLAN_INFO_DTYPE)
+    _native.call("sh_plan_describe", table.ctypes.data, len(table), info.ctypes.data)
+    return {k: int(info[0][k]) for k in PLAN_INFO_DTYPE.names}
+
+
+def test_plan_describe_counts_and_extents():
+    info = describe([
+        (KIND_I8_ROWSCALE_BF16, 8, 0, 3072, 3072, 0, 0),
+        (KIND_I8_ROWSCALE_BF16, 8 + 3072 * 3072, 2 * 3072 * 3072, 1000, 77, 0, 3072),
+    ])
+    n = 3072 * 3072 + 77000
+    assert info["elements"] == n
+    assert info["algo_bytes"] == n * 3 + 4 * (3072 + 1000)
+    assert info["src_extent"] == 8 + n
+    assert info["dst_extent"] == 2 * n
+    assert info["scale_extent"] == 4072
+    assert info["n_tiles"] == 3072 * 3072 // 16384 + (77000 + 16383) // 16384
+    assert info["kind_mask"] == 1 << KIND_I8_ROWSCALE_BF16
+
+
+def test_plan_describe_padded_source_extent():
+    info = describe([(KIND_I8_ROWSCALE_BF16, 0, 0, 6, 10, 16, 0)])
+    assert info["src_extent"] == 5 * 16 + 10
+    assert info["dst_extent"] == 6 * 10 * 2
+
+
+def test_plan_describe_splits_oversize_regions():
+    # 2^31 + 2^20 fp32 elements → more than one descriptor, same totals
+    n = (1 << 31) + (1 << 20)
+    info = describe([(KIND_F32_BF16, 0, 0, 1, n, 0, 0)])
+    assert info["n_desc"] == 3
+    assert info["elements"] == n
+    assert info["src_extent"] == 4 * n and info["dst_extent"] == 2 * n
+    info = describe([(KIND_I8_ROWSCALE_BF16, 0, 0, 300000, 12288, 0, 0)])
+    assert info["n_desc"] == 2
+    assert info["scale_extent"] == 300000
+
+
+def test_plan_describe_all_kinds_and_empty_regions():
+    info = describe([
+        (KIND_I8_ROWSCALE_F32, 0, 0, 2, 16, 0, 0),
+        (KIND_F32_BF16, 32, 128, 1, 5, 0, 0),
+        (KIND_BF16_F32, 52, 138, 1, 3, 0, 0),
+        (KIND_COPY_BYTES, 58, 150, 1, 7, 0, 0),
+        (KIND_ZERO_BYTES, 0, 157, 1, 9, 0, 0),
+        (KIND_F32_BF16, 0, 0, 0, 5, 0, 0),  # empty: dropped
+    ])
+    assert info["n_desc"] == 5
+    assert info["dst_extent"] == 166
+    assert info["src_extent"] == 65
+
+
+@pytest.mark.parametrize("bad", [
+    (9, 0, 0, 1, 4, 0, 0),                        # unknown kind
+    (KIND_I8_ROWSCALE_BF16, 0, 0, 4, 16, 8, 0),   # src_ld < cols
+    (KIND_F32_BF16, 0, 0, 2, 16, 32, 0),          # strided non-int8 region
+])
+def test_plan_describe_rejects_bad_descriptors(bad):
+    with pytest.raises(ValueError):
+        describe([bad])
+
+
+def _div(d: int, n: np.ndarray) -> np.ndarray:
+    n = np.ascontiguousarray(n, dtype=np.uint32)
+    q = np.zeros_like(n)
+    _native.call("sh_index_div", d, n.ctypes.data, q.ctypes.data, n.size)
+    return q
+
+
+def test_index_division_is_exact():
+    rng = np.random.default_rng(0)
+    divisors = [1, 2, 3, 7, 16, 77, 1000, 3072, 12288, 65535, 65536, 65537, 2**31 - 1, 2**31, 2**32 - 1]
+    divisors += [int(x) for x in rng.integers(1, 2**32, 20, dtype=np.uint64)]
+    for d in divisors:
+        n = np.concatenate([
+            rng.integers(0, 2**32, 20000, dtype=np.uint64),
+            np.array([0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d, 2**32 - 1, 2**32 - 2], dtype=np.uint64) % 2**32,
+            (np.arange(1, 2000, dtype=np.uint64) * d) % 2**32,
+            (np.arange(1, 2000, dtype=np.uint64) * d - 1) % 2**32,
+        ]).astype(np.uint32)
+        np.testing.assert_array_equal(_div(d, n), n // np.uint32(d), err_msg=f"d={d}")
+
+
+def test_index_division_rejects_zero():
+    with pytest.raises(ValueError):
+        _div(0, np.array([1], np.uint32))
