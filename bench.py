@@ -149,6 +149,43 @@ def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
     }
 
 
+def profile_pass(args) -> int:
+    """Three launches each of the dequant and cast kernels over config 2, and of a
+    plain 1 GiB byte copy through the same unpack machinery (the calibration
+    kernel for HBM byte counters)."""
+    import torch
+
+    from stagehand_amd.unpack import (KIND_COPY_BYTES, UnpackPlan, dequant_i8_rowscale_bf16, make_descs,
+                                      unpack_cast_f32_bf16)
+    from stagehand_amd.workloads import config2_descs, config2_device_inputs, config2_regions
+
+    regions = config2_regions()
+    n = sum(g.numel for g in regions)
+    dst = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    plan = UnpackPlan(config2_descs(regions, "dequant"))
+    src, scales = config2_device_inputs(regions, "dequant", seed=args.seed)
+    for _ in range(3):
+        dequant_i8_rowscale_bf16(plan, src, scales, dst)
+    torch.cuda.synchronize()
+    del src, scales
+    cplan = UnpackPlan(config2_descs(regions, "cast"))
+    csrc, _ = config2_device_inputs(regions, "cast", seed=args.seed + 1)
+    for _ in range(3):
+        unpack_cast_f32_bf16(cplan, csrc, dst)
+    torch.cuda.synchronize()
+    del csrc
+    nbytes = 1 << 30
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    kplan = UnpackPlan(make_descs([(KIND_COPY_BYTES, 0, 0, 1, nbytes, 0, 0)]))
+    for _ in range(3):
+        kplan.run(a, b)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_pass": True, "dequant_algo_bytes": plan.info["algo_bytes"],
+                      "cast_algo_bytes": cplan.info["algo_bytes"], "copy_bytes_each_way": nbytes}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,6 +195,8 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--skip-extras", action="store_true", help="omit cast / PCIe / D2D measurements")
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="only launch each kernel a few times (dequant, cast, 1 GiB copy) for counter runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -175,6 +214,8 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if args.profile_pass:
+        return profile_pass(args)
 
     regions = config2_regions()
     n = sum(g.numel for g in regions)

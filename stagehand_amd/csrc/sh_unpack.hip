@@ -8,15 +8,17 @@
 //   zero-fill         src/stagehand/scheduler.py:240, 276-297, 325
 //
 // Work decomposition. Every descriptor covers rows*cols elements, cut into
-// tiles of kThreads * kChunk * kUnroll elements; a host-built tile map gives
+// tiles of kThreads * kUnroll * chunk elements; a host-built tile map gives
 // each workgroup its descriptor in O(1) (one scalar load), and the descriptor
 // itself is a 64-byte scalar load, so all per-region state lives in SGPRs.
-// Each thread moves kUnroll chunks of 16 elements; all loads of a thread are
-// issued before the first conversion, so a wave keeps 4 x 16 B (int8) or
-// 4 x 64 B (fp32) per lane in flight. Loads and stores are 128-bit; the
-// hardware's unaligned-access mode lets them start at any byte offset, which
-// the reference layout needs (it has no padding, so int8 regions start at
-// arbitrary offsets). This is pure streaming: no LDS and no MFMA.
+// Each thread moves kUnroll chunks; all loads of a thread are issued before
+// the first conversion. Loads and stores are 128-bit (64-bit for the cast's
+// 8-byte output); the hardware's unaligned-access mode lets them start at any
+// byte offset, which the reference layout needs (it has no padding, so int8
+// regions start at arbitrary offsets). With int8 chunks of 16, every chunk of
+// a row whose length is a multiple of 16 needs one row scale, loaded once per
+// thread; shorter or ragged rows take an element-wise path. This is pure
+// streaming: no LDS (the scale is one load per chunk) and no MFMA.
 //
 // Numerics. The dequant is computed exactly as the reference's torch CPU ops:
 // f32(q) exactly, then an IEEE fp32 subtract of the zero point (skipped when
@@ -43,23 +45,59 @@
 
 namespace {
 
-constexpr uint32_t kThreads = 256;
-constexpr uint32_t kChunk = 16;  // elements per thread per chunk (16-element kinds)
-constexpr uint32_t kChunkBytes = 64;  // bytes per thread per chunk (byte kinds)
-constexpr uint32_t kUnroll = 4;
-constexpr uint32_t kTileElems = kThreads * kChunk * kUnroll;       // 16384
-constexpr uint32_t kTileBytes = kThreads * kChunkBytes * kUnroll;  // 65536
+// Launch shape, chosen by measurement on MI355X over the config-2 slab: one
+// chunk per thread and many short-lived 512-thread workgroups stream best
+// (dequant 16 int8 → 32 B of bf16 per thread; cast 4 fp32 → 8 B per thread).
+// Persistent grids, deeper per-thread unrolling, wider cast chunks and
+// non-temporal loads/stores each measured 5-25% slower.
+#ifndef SH_UNPACK_THREADS
+#define SH_UNPACK_THREADS 512
+#endif
+#ifndef SH_UNPACK_UNROLL
+#define SH_UNPACK_UNROLL 1
+#endif
+#ifndef SH_CHUNK_I8
+#define SH_CHUNK_I8 16
+#endif
+#ifndef SH_CHUNK_F32
+#define SH_CHUNK_F32 4
+#endif
+
+constexpr uint32_t kThreads = SH_UNPACK_THREADS;
+constexpr uint32_t kUnroll = SH_UNPACK_UNROLL;
+constexpr uint32_t kChunkI8 = SH_CHUNK_I8;     // int8 elements per thread per chunk
+constexpr uint32_t kChunkF32 = SH_CHUNK_F32;   // fp32 elements per thread per chunk (cast)
+constexpr uint32_t kChunkB16 = 16;             // bf16 elements per thread per chunk (widen)
+constexpr uint32_t kChunkBytes = 64;           // bytes per thread per chunk (copy / zero)
+static_assert(kChunkI8 % 4 == 0 && kChunkF32 % 4 == 0, "chunks are whole 32-bit words");
 constexpr uint64_t kMaxDescElems = 1ull << 31;
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t chunk_of(uint32_t kind) {
+  return (kind == SH_KIND_I8_ROWSCALE_BF16 || kind == SH_KIND_I8_ROWSCALE_F32) ? kChunkI8
+         : kind == SH_KIND_F32_BF16                                              ? kChunkF32
+         : kind == SH_KIND_BF16_F32                                              ? kChunkB16
+                                                                                 : kChunkBytes;
+}
+constexpr uint32_t tile_of(uint32_t kind) { return kThreads * kUnroll * chunk_of(kind); }
 
-__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
-  u32x4 v;
-  __builtin_memcpy(&v, p, 16);
+// NB bytes as 32-bit words; loaded and stored with unaligned-capable 128-bit
+// (or 64-bit) vector memory operations.
+template <uint32_t NB>
+struct Words {
+  uint32_t w[NB / 4];
+};
+
+template <uint32_t NB>
+__device__ __forceinline__ Words<NB> ldw(const uint8_t* p) {
+  Words<NB> v;
+  __builtin_memcpy(&v, p, NB);
   return v;
 }
 
-__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_memcpy(p, &v, 16); }
+template <uint32_t NB>
+__device__ __forceinline__ void stw(uint8_t* p, const Words<NB>& v) {
+  __builtin_memcpy(p, &v, NB);
+}
 
 // Rounded bf16 in bits 31..16 (low half is garbage): u + 0x7FFF + lsb.
 __device__ __forceinline__ uint32_t rne_hi(float x) {
@@ -78,7 +116,7 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t lo, uint32_t hi) {
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(rne_hi_nan(x) >> 16); }
 
-__device__ __forceinline__ float i8_at(uint32_t word, int byte) {
+__device__ __forceinline__ float i8_at(uint32_t word, uint32_t byte) {
   return (float)(int32_t)(int8_t)(uint8_t)(word >> (8 * byte));
 }
 
@@ -90,38 +128,27 @@ __device__ __forceinline__ float dq(float q, float s, float z) {
 
 // ── INT8 row-scale dequant ────────────────────────────────────────────────
 
-template <bool OUT_BF16, bool HAS_ZP, bool NANCHK>
-__device__ __forceinline__ void dq16_store(u32x4 q, float s, float z, uint8_t* out) {
+// One chunk of C int8 values of a single row → C outputs.
+template <uint32_t C, bool OUT_BF16, bool HAS_ZP, bool NANCHK>
+__device__ __forceinline__ void dq_chunk_store(const Words<C>& q, float s, float z, uint8_t* out) {
   if (OUT_BF16) {
-    u32x4 o0, o1;
+    Words<2 * C> o;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t word = q[w];
+    for (uint32_t w = 0; w < C / 4; ++w) {
+      const uint32_t word = q.w[w];
       const float f0 = dq<HAS_ZP>(i8_at(word, 0), s, z);
       const float f1 = dq<HAS_ZP>(i8_at(word, 1), s, z);
       const float f2 = dq<HAS_ZP>(i8_at(word, 2), s, z);
       const float f3 = dq<HAS_ZP>(i8_at(word, 3), s, z);
-      const uint32_t a = NANCHK ? pack_hi(rne_hi_nan(f0), rne_hi_nan(f1)) : pack_hi(rne_hi(f0), rne_hi(f1));
-      const uint32_t b = NANCHK ? pack_hi(rne_hi_nan(f2), rne_hi_nan(f3)) : pack_hi(rne_hi(f2), rne_hi(f3));
-      if (w < 2) {
-        o0[2 * w] = a;
-        o0[2 * w + 1] = b;
-      } else {
-        o1[2 * (w - 2)] = a;
-        o1[2 * (w - 2) + 1] = b;
-      }
+      o.w[2 * w] = NANCHK ? pack_hi(rne_hi_nan(f0), rne_hi_nan(f1)) : pack_hi(rne_hi(f0), rne_hi(f1));
+      o.w[2 * w + 1] = NANCHK ? pack_hi(rne_hi_nan(f2), rne_hi_nan(f3)) : pack_hi(rne_hi(f2), rne_hi(f3));
     }
-    st16(out, o0);
-    st16(out + 16, o1);
+    stw<2 * C>(out, o);
   } else {
+    Words<4 * C> o;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t word = q[w];
-      u32x4 o;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) o[b] = __float_as_uint(dq<HAS_ZP>(i8_at(word, b), s, z));
-      st16(out + 16 * w, o);
-    }
+    for (uint32_t j = 0; j < C; ++j) o.w[j] = __float_as_uint(dq<HAS_ZP>(i8_at(q.w[j / 4], j % 4), s, z));
+    stw<4 * C>(out, o);
   }
 }
 
@@ -140,6 +167,8 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
                                         const uint8_t* __restrict__ src,
                                         const float* __restrict__ scales,
                                         const float* __restrict__ zps, uint8_t* __restrict__ dst) {
+  constexpr uint32_t C = kChunkI8;
+  constexpr uint32_t kOutBytes = OUT_BF16 ? 2 : 4;
   const uint32_t cols = d.cols;
   const uint32_t numel = d.rows * cols;
   const uint32_t ld = d.src_ld ? d.src_ld : cols;
@@ -147,21 +176,20 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
   uint8_t* o = dst + d.dst_off;
   const float* sc = scales + d.scale_off;
   const float* zp = HAS_ZP ? zps + d.scale_off : nullptr;
-  constexpr uint32_t kOutBytes = OUT_BF16 ? 2 : 4;
-  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
+  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
 
-  if (ld == cols && (cols % kChunk) == 0) {
-    // Every chunk lies inside one row: one scale per 16 elements.
-    u32x4 q[kUnroll];
+  if (ld == cols && (cols % C) == 0) {
+    // Every chunk lies inside one row: one scale per chunk.
+    Words<C> q[kUnroll];
     float sv[kUnroll], zv[kUnroll];
 #pragma unroll
     for (uint32_t k = 0; k < kUnroll; ++k) {
-      const uint32_t e = e0 + k * (kThreads * kChunk);
-      if (e < numel) q[k] = ld16(s + e);
+      const uint32_t e = e0 + k * (kThreads * C);
+      if (e < numel) q[k] = ldw<C>(s + e);
     }
 #pragma unroll
     for (uint32_t k = 0; k < kUnroll; ++k) {
-      const uint32_t e = e0 + k * (kThreads * kChunk);
+      const uint32_t e = e0 + k * (kThreads * C);
       if (e < numel) {
         const uint32_t r = sh::udiv(e, d.div_magic);
         sv[k] = sc[r];
@@ -170,59 +198,55 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
     }
 #pragma unroll
     for (uint32_t k = 0; k < kUnroll; ++k) {
-      const uint32_t e = e0 + k * (kThreads * kChunk);
+      const uint32_t e = e0 + k * (kThreads * C);
       if (e < numel) {
         uint8_t* out = o + (size_t)e * kOutBytes;
-        // Finite scale and zero point cannot produce NaN from a finite q.
+        // A finite scale and zero point cannot turn a finite q into NaN.
         if (__builtin_isfinite(sv[k]) && (!HAS_ZP || __builtin_isfinite(zv[k])))
-          dq16_store<OUT_BF16, HAS_ZP, false>(q[k], sv[k], zv[k], out);
+          dq_chunk_store<C, OUT_BF16, HAS_ZP, false>(q[k], sv[k], zv[k], out);
         else
-          dq16_store<OUT_BF16, HAS_ZP, true>(q[k], sv[k], zv[k], out);
+          dq_chunk_store<C, OUT_BF16, HAS_ZP, true>(q[k], sv[k], zv[k], out);
       }
     }
     return;
   }
 
-  // Rows shorter than or not a multiple of 16, or a padded source (ld > cols):
-  // element-wise with the row tracked incrementally inside each chunk.
+  // Rows that are not a multiple of the chunk, or a padded source (ld > cols):
+  // element-wise, with the row tracked incrementally inside each chunk.
 #pragma unroll 1
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t e = e0 + k * (kThreads * kChunk);
+    const uint32_t e = e0 + k * (kThreads * C);
     if (e >= numel) break;
     uint32_t r = sh::udiv(e, d.div_magic);
     uint32_t c = e - r * cols;
-    const uint32_t n = min(kChunk, numel - e);
-    if (ld == cols && n == kChunk) {
-      const u32x4 q = ld16(s + e);
+    const uint32_t n = min(C, numel - e);
+    if (ld == cols && n == C) {
+      const Words<C> q = ldw<C>(s + e);
       if (OUT_BF16) {
-        uint32_t hw[kChunk];
+        uint32_t hw[C];
 #pragma unroll
-        for (uint32_t j = 0; j < kChunk; ++j) {
-          const float f = dq<HAS_ZP>(i8_at(q[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f);
-          hw[j] = rne_hi_nan(f);
+        for (uint32_t j = 0; j < C; ++j) {
+          hw[j] = rne_hi_nan(dq<HAS_ZP>(i8_at(q.w[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f));
           if (++c == cols) {
             c = 0;
             ++r;
           }
         }
-        u32x4 o0, o1;
+        Words<2 * C> ow;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          o0[w] = pack_hi(hw[2 * w], hw[2 * w + 1]);
-          o1[w] = pack_hi(hw[8 + 2 * w], hw[8 + 2 * w + 1]);
-        }
-        st16(o + (size_t)e * 2, o0);
-        st16(o + (size_t)e * 2 + 16, o1);
+        for (uint32_t w = 0; w < C / 2; ++w) ow.w[w] = pack_hi(hw[2 * w], hw[2 * w + 1]);
+        stw<2 * C>(o + (size_t)e * 2, ow);
       } else {
+        Words<4 * C> ow;
 #pragma unroll
-        for (uint32_t j = 0; j < kChunk; ++j) {
-          const float f = dq<HAS_ZP>(i8_at(q[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f);
-          store_elem<false>(o, e + j, f);
+        for (uint32_t j = 0; j < C; ++j) {
+          ow.w[j] = __float_as_uint(dq<HAS_ZP>(i8_at(q.w[j / 4], j % 4), sc[r], HAS_ZP ? zp[r] : 0.0f));
           if (++c == cols) {
             c = 0;
             ++r;
           }
         }
+        stw<4 * C>(o + (size_t)e * 4, ow);
       }
     } else {
       for (uint32_t j = 0; j < n; ++j) {
@@ -242,33 +266,26 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
 __device__ __forceinline__ void tile_f32_bf16(const sh_unpack_desc& d, uint32_t local,
                                               const uint8_t* __restrict__ src,
                                               uint8_t* __restrict__ dst) {
+  constexpr uint32_t C = kChunkF32;
   const uint32_t numel = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
-  u32x4 v[kUnroll][4];
+  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
+  Words<4 * C> v[kUnroll];
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t e = e0 + k * (kThreads * kChunk);
-    if (e + kChunk <= numel) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[k][i] = ld16(s + (size_t)e * 4 + 16 * i);
-    }
+    const uint32_t e = e0 + k * (kThreads * C);
+    if (e + C <= numel) v[k] = ldw<4 * C>(s + (size_t)e * 4);
   }
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t e = e0 + k * (kThreads * kChunk);
-    if (e + kChunk <= numel) {
-      u32x4 o0, o1;
+    const uint32_t e = e0 + k * (kThreads * C);
+    if (e + C <= numel) {
+      Words<2 * C> ow;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        o0[2 * i] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i][0])), rne_hi_nan(__uint_as_float(v[k][i][1])));
-        o0[2 * i + 1] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i][2])), rne_hi_nan(__uint_as_float(v[k][i][3])));
-        o1[2 * i] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i + 2][0])), rne_hi_nan(__uint_as_float(v[k][i + 2][1])));
-        o1[2 * i + 1] = pack_hi(rne_hi_nan(__uint_as_float(v[k][i + 2][2])), rne_hi_nan(__uint_as_float(v[k][i + 2][3])));
-      }
-      st16(o + (size_t)e * 2, o0);
-      st16(o + (size_t)e * 2 + 16, o1);
+      for (uint32_t w = 0; w < C / 2; ++w)
+        ow.w[w] = pack_hi(rne_hi_nan(__uint_as_float(v[k].w[2 * w])), rne_hi_nan(__uint_as_float(v[k].w[2 * w + 1])));
+      stw<2 * C>(o + (size_t)e * 2, ow);
     } else if (e < numel) {
       for (uint32_t j = e; j < numel; ++j) {
         float x;
@@ -285,35 +302,28 @@ __device__ __forceinline__ void tile_f32_bf16(const sh_unpack_desc& d, uint32_t 
 __device__ __forceinline__ void tile_bf16_f32(const sh_unpack_desc& d, uint32_t local,
                                               const uint8_t* __restrict__ src,
                                               uint8_t* __restrict__ dst) {
+  constexpr uint32_t C = kChunkB16;
   const uint32_t numel = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t e0 = local * kTileElems + threadIdx.x * kChunk;
-  u32x4 v[kUnroll][2];
+  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
+  Words<2 * C> v[kUnroll];
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t e = e0 + k * (kThreads * kChunk);
-    if (e + kChunk <= numel) {
-      v[k][0] = ld16(s + (size_t)e * 2);
-      v[k][1] = ld16(s + (size_t)e * 2 + 16);
-    }
+    const uint32_t e = e0 + k * (kThreads * C);
+    if (e + C <= numel) v[k] = ldw<2 * C>(s + (size_t)e * 2);
   }
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t e = e0 + k * (kThreads * kChunk);
-    if (e + kChunk <= numel) {
+    const uint32_t e = e0 + k * (kThreads * C);
+    if (e + C <= numel) {
+      Words<4 * C> ow;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          u32x4 w;
-          w[0] = v[k][h][2 * p] << 16;
-          w[1] = v[k][h][2 * p] & 0xFFFF0000u;
-          w[2] = v[k][h][2 * p + 1] << 16;
-          w[3] = v[k][h][2 * p + 1] & 0xFFFF0000u;
-          st16(o + (size_t)e * 4 + 32 * h + 16 * p, w);
-        }
+      for (uint32_t w = 0; w < C / 2; ++w) {
+        ow.w[2 * w] = v[k].w[w] << 16;
+        ow.w[2 * w + 1] = v[k].w[w] & 0xFFFF0000u;
       }
+      stw<4 * C>(o + (size_t)e * 4, ow);
     } else if (e < numel) {
       for (uint32_t j = e; j < numel; ++j) {
         uint16_t b;
@@ -331,25 +341,29 @@ template <bool ZERO>
 __device__ __forceinline__ void tile_bytes(const sh_unpack_desc& d, uint32_t local,
                                            const uint8_t* __restrict__ src,
                                            uint8_t* __restrict__ dst) {
+  constexpr uint32_t C = kChunkBytes;
   const uint32_t nbytes = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t b0 = local * kTileBytes + threadIdx.x * kChunkBytes;
-  u32x4 v[kUnroll][4];
+  const uint32_t b0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
+  Words<C> v[kUnroll];
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t b = b0 + k * (kThreads * kChunkBytes);
-    if (b + kChunkBytes <= nbytes) {
+    const uint32_t b = b0 + k * (kThreads * C);
+    if (b + C <= nbytes) {
+      if (ZERO) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[k][i] = ZERO ? u32x4{0, 0, 0, 0} : ld16(s + b + 16 * i);
+        for (uint32_t w = 0; w < C / 4; ++w) v[k].w[w] = 0;
+      } else {
+        v[k] = ldw<C>(s + b);
+      }
     }
   }
 #pragma unroll
   for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t b = b0 + k * (kThreads * kChunkBytes);
-    if (b + kChunkBytes <= nbytes) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st16(o + b + 16 * i, v[k][i]);
+    const uint32_t b = b0 + k * (kThreads * C);
+    if (b + C <= nbytes) {
+      stw<C>(o + b, v[k]);
     } else if (b < nbytes) {
       for (uint32_t j = b; j < nbytes; ++j) o[j] = ZERO ? (uint8_t)0 : s[j];
     }
@@ -472,13 +486,13 @@ int build_table(const sh_unpack_desc* descs, uint32_t n, std::vector<sh_unpack_d
   table.clear();
   table.reserve(n);
   info = sh_plan_info{};
-  info.tile_elems = kTileElems;
+  info.tile_elems = tile_of(SH_KIND_I8_ROWSCALE_BF16);
   uint64_t tiles = 0;
 
   auto push = [&](sh_unpack_desc d) -> int {
     const uint64_t numel = (uint64_t)d.rows * d.cols;
     d.div_magic = sh::udiv_magic(d.cols);
-    const uint64_t per_tile = is_bytes(d.kind) ? kTileBytes : kTileElems;
+    const uint64_t per_tile = tile_of(d.kind);
     const uint64_t nt = (numel + per_tile - 1) / per_tile;
     if (tiles + nt > 0x7FFFFFFFull)
       return sh::fail(SH_ERR_INVALID, "%s: plan needs more than 2^31-1 tiles", who);
