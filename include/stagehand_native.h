@@ -182,6 +182,99 @@ int sh_unpack_cast_f32_bf16(const sh_plan* plan,
                             const float* src, size_t src_bytes,
                             uint16_t* dst, size_t dst_bytes, void* stream);
 
+/* ───────────────────────── pinned slab pool ─────────────────────────
+ * Replaces the torch pinned-tensor pool of src/stagehand/pool.py:42-246
+ * (PinnedPool.__init__ :58-116, acquire :122-175, release :181-196,
+ * stats :202-212, shutdown :218-226). One pinned region (hipHostMalloc) cut
+ * into equal slabs; pinned == 0 gives ordinary aligned host memory (the
+ * reference's no-GPU fallback, pool.py:87). */
+typedef struct sh_pool sh_pool;
+typedef struct sh_pool_stats {
+  uint64_t total;        /* slabs */
+  uint64_t free;         /* slabs on the free list */
+  uint64_t in_use;       /* acquired or awaiting their release event */
+  uint64_t peak_in_use;
+  uint64_t wait_count;   /* acquires that had to wait */
+  uint64_t fenced;       /* released slabs whose release event has not completed */
+  double total_wait_ms;
+  uint64_t slab_bytes;
+  uint64_t pinned;
+} sh_pool_stats;
+
+int sh_pool_create(uint32_t num_slabs, uint64_t slab_bytes, int pinned, sh_pool** out);
+int sh_pool_destroy(sh_pool* pool);
+int sh_pool_slab_ptr(sh_pool* pool, uint32_t slab, void** ptr);
+/* Blocks until a slab is free (timeout_ms < 0: no limit; SH_ERR_TIMEOUT when it
+ * expires). waited_ms (may be NULL) receives the time spent waiting. */
+int sh_pool_acquire(sh_pool* pool, int64_t timeout_ms, uint32_t* slab, double* waited_ms);
+int sh_pool_release(sh_pool* pool, uint32_t slab);
+/* No reference counterpart: the slab returns to the free list once all work
+ * queued on `stream` so far has completed (an event the pool records), so the
+ * host need not wait for an H2D copy before recycling its source slab. */
+int sh_pool_release_after(sh_pool* pool, uint32_t slab, void* stream);
+int sh_pool_get_stats(sh_pool* pool, sh_pool_stats* stats);
+
+/* Multi-threaded host memcpy of a batch of (dst, src, bytes) items, used to
+ * gather a block's parameters into its pinned slab (the per-parameter host
+ * copy_ loops of src/stagehand/scheduler.py:168-181, 203-241, 263-325). */
+typedef struct sh_copy_item {
+  void* dst;
+  const void* src;
+  uint64_t bytes;
+} sh_copy_item;
+int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threads);
+
+/* ───────────────────────── block loader ─────────────────────────
+ * A native worker thread that performs a block load end to end: gather the
+ * block's parameter bytes into a pinned slab (multi-threaded host copy), H2D
+ * the slab on the loader's copy stream, and, with a plan, unpack it into the
+ * destination on the loader's unpack stream. Replaces the synchronous host
+ * staging + copy + host wait of src/stagehand/scheduler.py:953-1031,
+ * src/stagehand/transfer.py:108-143 / 193-217 and the prefetch half of
+ * turbo_src/engine.rs:202-282.
+ *
+ * pieces[i].dst is a BYTE OFFSET inside the slab (not a pointer); src is a
+ * host pointer that must stay valid until the ticket is issued (sh_loader_query
+ * no longer returns SH_ERR_NOT_READY for the staging phase, i.e. after
+ * sh_loader_stream_wait / sh_loader_sync / a successful query).
+ * The source streams through the pool in slab-sized chunks (a block may be
+ * larger than one slab; the reference requires it to fit one, pool.py:133-175
+ * with scheduler.py:970). Without a plan the src_bytes are copied to dst; with
+ * a plan they are copied to `staging` (device) and unpacked into dst, with the
+ * fp32 scales / zero points read from staging + scale_off / zp_off
+ * (zp_off < 0: no zero points). The copy waits for the work queued on
+ * `wait_stream` at submit time (the destination's allocation stream). */
+typedef struct sh_load_request {
+  const sh_copy_item* pieces;
+  uint64_t n_pieces;
+  uint64_t src_bytes;
+  const sh_plan* plan;
+  void* staging;
+  uint64_t staging_bytes;
+  void* dst;
+  uint64_t dst_bytes;
+  int64_t scale_off;
+  int64_t zp_off;
+  uint64_t n_scale;
+  int32_t copy_threads;  /* host copy threads for this request; <= 0: loader default */
+  int32_t reserved;
+} sh_load_request;
+
+typedef struct sh_loader sh_loader;
+int sh_loader_create(sh_pool* pool, int copy_threads, sh_loader** out);
+int sh_loader_destroy(sh_loader* loader);
+int sh_loader_streams(sh_loader* loader, void** copy_stream, void** unpack_stream);
+int sh_loader_submit(sh_loader* loader, const sh_load_request* req, void* wait_stream, uint64_t* ticket);
+/* SH_OK once the destination is written, SH_ERR_NOT_READY before. */
+int sh_loader_query(sh_loader* loader, uint64_t ticket);
+/* Makes `stream` wait for the load on the device (the host waits only until
+ * the worker has issued it). */
+int sh_loader_stream_wait(sh_loader* loader, uint64_t ticket, void* stream);
+/* Host waits until the destination is written. */
+int sh_loader_sync(sh_loader* loader, uint64_t ticket);
+/* Forgets a ticket (waits for its device work first). */
+int sh_loader_release(sh_loader* loader, uint64_t ticket);
+
 /* Host copy of the kernels' row-index division (floor(n[i] / d) through the
  * 64-bit multiplicative inverse stored in sh_unpack_desc.div_magic), exported
  * so the index arithmetic can be checked on a CPU. No reference counterpart. */

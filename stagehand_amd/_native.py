@@ -127,7 +127,39 @@ _SIGNATURES: dict[str, list] = {
     "sh_unpack": [_vp, _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp],
     "sh_dequant_i8_rowscale_bf16": [_vp, _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp],
     "sh_unpack_cast_f32_bf16": [_vp, _vp, _sz, _vp, _sz, _vp],
+    "sh_pool_create": [_u32, ctypes.c_uint64, _i32, ctypes.POINTER(_vp)],
+    "sh_pool_destroy": [_vp],
+    "sh_pool_slab_ptr": [_vp, _u32, ctypes.POINTER(_vp)],
+    "sh_pool_acquire": [_vp, ctypes.c_int64, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_double)],
+    "sh_pool_release": [_vp, _u32],
+    "sh_pool_release_after": [_vp, _u32, _vp],
+    "sh_pool_get_stats": [_vp, _vp],
+    "sh_host_copy_batch": [_vp, _sz, _i32],
+    "sh_loader_create": [_vp, _i32, ctypes.POINTER(_vp)],
+    "sh_loader_destroy": [_vp],
+    "sh_loader_streams": [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
+    "sh_loader_submit": [_vp, _vp, _vp, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_loader_query": [_vp, ctypes.c_uint64],
+    "sh_loader_stream_wait": [_vp, ctypes.c_uint64, _vp],
+    "sh_loader_sync": [_vp, ctypes.c_uint64],
+    "sh_loader_release": [_vp, ctypes.c_uint64],
 }
+
+# Mirror of `struct sh_load_request`.
+LOAD_REQUEST_DTYPE = np.dtype([
+    ("pieces", "<u8"), ("n_pieces", "<u8"), ("src_bytes", "<u8"), ("plan", "<u8"), ("staging", "<u8"),
+    ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
+    ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"),
+])
+
+# Mirror of `struct sh_pool_stats`.
+POOL_STATS_DTYPE = np.dtype([
+    ("total", "<u8"), ("free", "<u8"), ("in_use", "<u8"), ("peak_in_use", "<u8"), ("wait_count", "<u8"),
+    ("fenced", "<u8"), ("total_wait_ms", "<f8"), ("slab_bytes", "<u8"), ("pinned", "<u8"),
+])
+
+# Mirror of `struct sh_copy_item`.
+COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])
 
 ABI_VERSION = 1
 

@@ -1,0 +1,59 @@
+"""VRAM watermark predicates over torch's allocator statistics
+(semantics of src/stagehand/budget.py:18-97).
+
+Block buffers are torch tensors, so ``torch.cuda.memory_allocated`` sees every
+byte the streaming path holds on the device, including device staging buffers
+of in-flight SquareQ loads.
+"""
+from __future__ import annotations
+
+import torch
+
+__all__ = ["BudgetManager"]
+
+
+class BudgetManager:
+    def __init__(self, high_watermark_mb: int = 22000, low_watermark_mb: int = 18000) -> None:
+        if high_watermark_mb <= low_watermark_mb:
+            raise ValueError(
+                f"high_watermark_mb ({high_watermark_mb}) must be greater than low_watermark_mb ({low_watermark_mb})"
+            )
+        self._high_watermark_mb = high_watermark_mb
+        self._low_watermark_mb = low_watermark_mb
+
+    def vram_used_mb(self) -> float:
+        if not torch.cuda.is_available():
+            return 0.0
+        return torch.cuda.memory_allocated() / (1024 * 1024)
+
+    def vram_reserved_mb(self) -> float:
+        if not torch.cuda.is_available():
+            return 0.0
+        return torch.cuda.memory_reserved() / (1024 * 1024)
+
+    def above_high_watermark(self) -> bool:
+        return self.vram_used_mb() >= self._high_watermark_mb
+
+    def below_low_watermark(self) -> bool:
+        return self.vram_used_mb() < self._low_watermark_mb
+
+    def headroom_mb(self) -> float:
+        return self._high_watermark_mb - self.vram_used_mb()
+
+    def should_evict(self) -> bool:
+        return self.above_high_watermark()
+
+    def can_prefetch(self) -> bool:
+        return not self.above_high_watermark()
+
+    @property
+    def high_watermark_mb(self) -> int:
+        return self._high_watermark_mb
+
+    @property
+    def low_watermark_mb(self) -> int:
+        return self._low_watermark_mb
+
+    def __repr__(self) -> str:
+        return (f"BudgetManager(high={self._high_watermark_mb}MB, low={self._low_watermark_mb}MB, "
+                f"used={self.vram_used_mb():.0f}MB)")

@@ -1,0 +1,40 @@
+"""Runtime configuration (same fields and defaults as src/stagehand/config.py:9-46).
+
+``copy_stream_priority`` is accepted for compatibility but every stream this
+package creates runs at the default priority (mixed-priority streams have hung
+on the target platform).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+__all__ = ["StagehandConfig"]
+
+
+@dataclass
+class StagehandConfig:
+    stagehand_enabled: bool = True
+    # host pinned pool
+    pinned_pool_mb: int = 8192
+    pinned_slab_mb: int = 256
+    pinned_slab_alignment: int = 512
+    # VRAM watermarks (torch.cuda.memory_allocated, MB)
+    vram_high_watermark_mb: int = 22000
+    vram_low_watermark_mb: int = 18000
+    # transfers
+    max_inflight_transfers: int = 2
+    copy_stream_priority: int = -1
+    # scheduling policy
+    policy: str = "static"
+    prefetch_window_blocks: int = 3
+    eviction_cooldown_steps: int = 2
+    # numeric guards
+    strict_bf16: bool = True
+    fail_on_dtype_promotion: bool = True
+    nan_inf_check: bool = True
+    # telemetry
+    telemetry_enabled: bool = True
+    telemetry_interval_steps: int = 10
+    telemetry_file: str = "stagehand_telemetry.jsonl"
+    # debug
+    debug_trace: bool = False

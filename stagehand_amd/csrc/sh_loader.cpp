@@ -1,0 +1,417 @@
+// Block loader: a native worker that stages a block's parameter bytes into a
+// pinned slab, copies the slab to the device on a copy stream and (for SquareQ
+// or fp32 sources) runs the unpack kernel on a second stream, all fenced by
+// HIP events.
+//
+// This replaces the synchronous host path of the reference's block loads:
+//   _stage_block_to_host       src/stagehand/scheduler.py:953-1031 (pool.acquire,
+//                              per-parameter host copy / cast / dequant into the slab)
+//   AsyncTransferEngine.submit_h2d  src/stagehand/transfer.py:108-143 (copy stream + event)
+//   AsyncTransferEngine.wait   src/stagehand/transfer.py:193-217 (host event sync)
+//   _finalize_gpu_load's slab release  src/stagehand/scheduler.py:1120-1124
+// and the turbo engine's prefetch of turbo_src/engine.rs:202-230 / 267-282.
+//
+// Pipeline per request (ticket):
+//   caller thread : record `ready` event on the caller's stream (the block's
+//                   destination buffer was allocated there), enqueue request.
+//   worker thread : acquire slab (blocks while every slab is busy; fenced
+//                   slabs come back as their H2D copies drain), gather the
+//                   pieces into the slab with the multi-threaded host copy,
+//                   copy stream: wait `ready`, H2D slab → staging (or → dst),
+//                   record `copied`; release the slab after `copied`;
+//                   unpack stream: wait `copied`, launch the plan, record `done`.
+//   caller thread : sh_loader_stream_wait(ticket, compute stream) makes the
+//                   compute stream wait for `done` without blocking the host.
+// The worker owns the host-side staging, so the Python hook thread never
+// copies weight bytes and never waits for a copy to finish.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <condition_variable>
+#include <cstring>
+#include <deque>
+#include <mutex>
+#include <new>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "sh_internal.h"
+#include "stagehand_native.h"
+
+namespace {
+
+enum class TicketState { Queued, Issued, Failed };
+
+struct Ticket {
+  TicketState state = TicketState::Queued;
+  hipEvent_t ready = nullptr;   // recorded on the caller's stream at submit
+  hipEvent_t copied = nullptr;  // H2D of the slab finished
+  hipEvent_t done = nullptr;    // destination fully written
+  int status = SH_OK;
+  std::string error;
+  // request
+  std::vector<sh_copy_item> pieces;
+  uint64_t src_bytes = 0;
+  const sh_plan* plan = nullptr;
+  void* staging = nullptr;
+  uint64_t staging_bytes = 0;
+  void* dst = nullptr;
+  uint64_t dst_bytes = 0;
+  int64_t scale_off = -1;
+  int64_t zp_off = -1;
+  uint64_t n_scale = 0;
+  int copy_threads = 1;
+};
+
+}  // namespace
+
+struct sh_loader {
+  sh_pool* pool = nullptr;
+  uint64_t slab_bytes = 0;
+  int device = 0;
+  int copy_threads = 1;
+  hipStream_t copy_stream = nullptr;
+  hipStream_t unpack_stream = nullptr;
+  std::mutex mu;
+  std::condition_variable cv;       // worker wakeup
+  std::condition_variable issued_cv;  // ticket state changes
+  std::deque<uint64_t> queue;
+  std::unordered_map<uint64_t, Ticket> tickets;
+  std::vector<hipEvent_t> spare_events;
+  uint64_t next_ticket = 1;
+  bool stop = false;
+  std::thread worker;
+};
+
+extern "C" int sh_unpack(const sh_plan* plan, const void* src, size_t src_bytes, const float* scales,
+                         const float* zero_points, size_t n_scale, void* dst, size_t dst_bytes, void* stream);
+
+namespace {
+
+hipError_t take_event(sh_loader* L, hipEvent_t* ev) {
+  if (!L->spare_events.empty()) {
+    *ev = L->spare_events.back();
+    L->spare_events.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreateWithFlags(ev, hipEventDisableTiming);
+}
+
+void give_events(sh_loader* L, Ticket& t) {
+  for (hipEvent_t* ev : {&t.ready, &t.copied, &t.done}) {
+    if (*ev) L->spare_events.push_back(*ev);
+    *ev = nullptr;
+  }
+}
+
+// Executes one request on the worker thread. Returns SH_OK or an error status
+// with `err` describing it. Runs without the loader lock held.
+int run_request(sh_loader* L, Ticket& t, std::string& err) {
+  auto hip_fail = [&](hipError_t e, const char* what) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "HIP error %d (%s) in %s", (int)e, hipGetErrorString(e), what);
+    err = buf;
+    return SH_ERR_HIP;
+  };
+  hipError_t e = hipSetDevice(L->device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+
+  // The source streams through the pool one slab-sized chunk at a time: gather
+  // the chunk's part of every piece into a slab, H2D it, release the slab
+  // after the copy. A block may therefore be larger than one slab; with two
+  // or more slabs the gather of chunk k+1 overlaps the H2D of chunk k.
+  void* h2d_dst = t.plan ? t.staging : t.dst;
+  e = hipStreamWaitEvent(L->copy_stream, t.ready, 0);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(ready)");
+  std::vector<sh_copy_item> items;
+  items.reserve(t.pieces.size());
+  for (uint64_t c0 = 0; c0 < t.src_bytes; c0 += L->slab_bytes) {
+    const uint64_t c1 = std::min<uint64_t>(t.src_bytes, c0 + L->slab_bytes);
+    uint32_t slab = 0;
+    double waited = 0;
+    int st = sh_pool_acquire(L->pool, -1, &slab, &waited);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      return st;
+    }
+    void* slab_ptr = nullptr;
+    sh_pool_slab_ptr(L->pool, slab, &slab_ptr);
+    items.clear();
+    for (const sh_copy_item& p : t.pieces) {
+      const uint64_t p0 = (uint64_t)(uintptr_t)p.dst, p1 = p0 + p.bytes;
+      const uint64_t a = std::max(p0, c0), b = std::min(p1, c1);
+      if (a >= b) continue;
+      sh_copy_item it;
+      it.dst = (uint8_t*)slab_ptr + (a - c0);
+      it.src = (const uint8_t*)p.src + (a - p0);
+      it.bytes = b - a;
+      items.push_back(it);
+    }
+    st = sh_host_copy_batch(items.data(), items.size(), t.copy_threads);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      sh_pool_release(L->pool, slab);
+      return st;
+    }
+    e = hipMemcpyAsync((uint8_t*)h2d_dst + c0, slab_ptr, c1 - c0, hipMemcpyHostToDevice, L->copy_stream);
+    if (e != hipSuccess) {
+      (void)hipStreamSynchronize(L->copy_stream);
+      sh_pool_release(L->pool, slab);
+      return hip_fail(e, "staging H2D copy");
+    }
+    st = sh_pool_release_after(L->pool, slab, L->copy_stream);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      return st;
+    }
+  }
+  e = hipEventRecord(t.copied, L->copy_stream);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord(copied)");
+  int st = SH_OK;
+  if (t.plan == nullptr) {
+    e = hipEventRecord(t.done, L->copy_stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
+    return SH_OK;
+  }
+  e = hipStreamWaitEvent(L->unpack_stream, t.copied, 0);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(copied)");
+  const uint8_t* stg = (const uint8_t*)t.staging;
+  const float* scales = t.scale_off >= 0 ? (const float*)(stg + t.scale_off) : nullptr;
+  const float* zps = t.zp_off >= 0 ? (const float*)(stg + t.zp_off) : nullptr;
+  st = sh_unpack(t.plan, t.staging, t.staging_bytes, scales, zps, t.n_scale, t.dst, t.dst_bytes, L->unpack_stream);
+  if (st != SH_OK) {
+    err = sh_last_error();
+    return st;
+  }
+  e = hipEventRecord(t.done, L->unpack_stream);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
+  return SH_OK;
+}
+
+void worker_loop(sh_loader* L) {
+  for (;;) {
+    uint64_t id = 0;
+    Ticket* t = nullptr;
+    {
+      std::unique_lock<std::mutex> lk(L->mu);
+      L->cv.wait(lk, [&] { return L->stop || !L->queue.empty(); });
+      if (L->queue.empty()) return;  // stop requested and drained
+      id = L->queue.front();
+      L->queue.pop_front();
+      t = &L->tickets.at(id);  // unordered_map references stay valid across inserts
+    }
+    std::string err;
+    const int st = run_request(L, *t, err);
+    {
+      std::lock_guard<std::mutex> lk(L->mu);
+      t->status = st;
+      t->error = err;
+      t->state = st == SH_OK ? TicketState::Issued : TicketState::Failed;
+      t->pieces.clear();
+      t->pieces.shrink_to_fit();
+    }
+    L->issued_cv.notify_all();
+  }
+}
+
+// Waits (caller thread) until the worker has issued or failed ticket `id`.
+// Returns SH_OK with *out set, or an error status.
+int wait_issued(sh_loader* L, uint64_t id, std::unique_lock<std::mutex>& lk, Ticket** out, const char* who) {
+  auto it = L->tickets.find(id);
+  if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "%s: unknown ticket %llu", who, (unsigned long long)id);
+  L->issued_cv.wait(lk, [&] { return it->second.state != TicketState::Queued; });
+  if (it->second.state == TicketState::Failed)
+    return sh::fail(it->second.status == SH_OK ? SH_ERR_HIP : it->second.status, "%s: load failed: %s", who,
+                    it->second.error.c_str());
+  *out = &it->second;
+  return SH_OK;
+}
+
+}  // namespace
+
+extern "C" int sh_loader_create(sh_pool* pool, int copy_threads, sh_loader** out) {
+  sh::clear_error();
+  if (pool == nullptr || out == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_create: NULL argument");
+  *out = nullptr;
+  sh_loader* L = new (std::nothrow) sh_loader();
+  if (L == nullptr) return sh::fail(SH_ERR_OOM, "sh_loader_create: out of host memory");
+  L->pool = pool;
+  L->copy_threads = copy_threads > 0 ? copy_threads : 1;
+  sh_pool_stats ps{};
+  if (int st = sh_pool_get_stats(pool, &ps)) {
+    delete L;
+    return st;
+  }
+  L->slab_bytes = ps.slab_bytes;
+  hipError_t e = hipGetDevice(&L->device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->copy_stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->unpack_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    if (L->copy_stream) (void)hipStreamDestroy(L->copy_stream);
+    if (L->unpack_stream) (void)hipStreamDestroy(L->unpack_stream);
+    delete L;
+    return sh::fail(SH_ERR_HIP, "sh_loader_create: HIP error %d (%s)", (int)e, hipGetErrorString(e));
+  }
+  L->worker = std::thread(worker_loop, L);
+  *out = L;
+  return SH_OK;
+}
+
+extern "C" int sh_loader_destroy(sh_loader* L) {
+  sh::clear_error();
+  if (L == nullptr) return SH_OK;
+  {
+    std::lock_guard<std::mutex> lk(L->mu);
+    L->stop = true;
+  }
+  L->cv.notify_all();
+  if (L->worker.joinable()) L->worker.join();
+  (void)hipStreamSynchronize(L->copy_stream);
+  (void)hipStreamSynchronize(L->unpack_stream);
+  for (auto& kv : L->tickets) give_events(L, kv.second);
+  for (hipEvent_t ev : L->spare_events) (void)hipEventDestroy(ev);
+  (void)hipStreamDestroy(L->copy_stream);
+  (void)hipStreamDestroy(L->unpack_stream);
+  delete L;
+  return SH_OK;
+}
+
+extern "C" int sh_loader_streams(sh_loader* L, void** copy_stream, void** unpack_stream) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_streams: loader is NULL");
+  if (copy_stream) *copy_stream = (void*)L->copy_stream;
+  if (unpack_stream) *unpack_stream = (void*)L->unpack_stream;
+  return SH_OK;
+}
+
+extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* wait_stream, uint64_t* ticket) {
+  sh::clear_error();
+  if (L == nullptr || req == nullptr || ticket == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: NULL argument");
+  if (req->n_pieces > 0 && req->pieces == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: pieces is NULL");
+  if (req->dst == nullptr && req->dst_bytes > 0) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: dst is NULL");
+  uint64_t need = 0;
+  for (uint64_t i = 0; i < req->n_pieces; ++i) {
+    const sh_copy_item& p = req->pieces[i];
+    const uint64_t end = (uint64_t)(uintptr_t)p.dst + p.bytes;
+    if (end < p.bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: piece %llu overflows", (unsigned long long)i);
+    if (p.bytes > 0 && p.src == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: piece %llu has no source", (unsigned long long)i);
+    need = need > end ? need : end;
+  }
+  if (need > req->src_bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: pieces end at %llu, past src_bytes %llu",
+                                             (unsigned long long)need, (unsigned long long)req->src_bytes);
+  if (req->plan != nullptr) {
+    sh_plan_info info{};
+    sh_plan_get_info(req->plan, &info);
+    if (req->staging == nullptr || req->staging_bytes < req->src_bytes)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: device staging buffer smaller than the source");
+    if (info.src_extent > req->src_bytes)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: plan reads %llu source bytes, only %llu are sent",
+                      (unsigned long long)info.src_extent, (unsigned long long)req->src_bytes);
+    if (req->dst_bytes < info.dst_extent)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: destination smaller than the plan's extent");
+    const bool has_i8 = (info.kind_mask & ((1u << SH_KIND_I8_ROWSCALE_BF16) | (1u << SH_KIND_I8_ROWSCALE_F32))) != 0;
+    if (has_i8) {
+      if (req->scale_off < 0 || (req->scale_off % 4) != 0 ||
+          (uint64_t)req->scale_off + 4 * req->n_scale > req->src_bytes || req->n_scale < info.scale_extent)
+        return sh::fail(SH_ERR_INVALID, "sh_loader_submit: scales are not inside the source or too few");
+      if (req->zp_off >= 0 && ((req->zp_off % 4) != 0 || (uint64_t)req->zp_off + 4 * req->n_scale > req->src_bytes))
+        return sh::fail(SH_ERR_INVALID, "sh_loader_submit: zero points are not inside the source");
+    }
+  } else if (req->dst_bytes < req->src_bytes) {
+    return sh::fail(SH_ERR_INVALID, "sh_loader_submit: destination smaller than the source bytes");
+  }
+
+  std::lock_guard<std::mutex> lk(L->mu);
+  const uint64_t id = L->next_ticket++;
+  Ticket& t = L->tickets[id];
+  hipError_t e = take_event(L, &t.ready);
+  if (e == hipSuccess) e = take_event(L, &t.copied);
+  if (e == hipSuccess) e = take_event(L, &t.done);
+  if (e == hipSuccess) e = hipEventRecord(t.ready, (hipStream_t)wait_stream);
+  if (e != hipSuccess) {
+    give_events(L, t);
+    L->tickets.erase(id);
+    return sh::fail(SH_ERR_HIP, "sh_loader_submit: HIP error %d (%s)", (int)e, hipGetErrorString(e));
+  }
+  t.pieces.assign(req->pieces, req->pieces + req->n_pieces);
+  t.src_bytes = req->src_bytes;
+  t.plan = req->plan;
+  t.staging = req->staging;
+  t.staging_bytes = req->staging_bytes;
+  t.dst = req->dst;
+  t.dst_bytes = req->dst_bytes;
+  t.scale_off = req->scale_off;
+  t.zp_off = req->zp_off;
+  t.n_scale = req->n_scale;
+  t.copy_threads = req->copy_threads > 0 ? req->copy_threads : L->copy_threads;
+  L->queue.push_back(id);
+  *ticket = id;
+  L->cv.notify_one();
+  return SH_OK;
+}
+
+extern "C" int sh_loader_query(sh_loader* L, uint64_t ticket) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_query: loader is NULL");
+  std::lock_guard<std::mutex> lk(L->mu);
+  auto it = L->tickets.find(ticket);
+  if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "sh_loader_query: unknown ticket %llu", (unsigned long long)ticket);
+  Ticket& t = it->second;
+  if (t.state == TicketState::Queued) return SH_ERR_NOT_READY;
+  if (t.state == TicketState::Failed) return sh::fail(t.status, "sh_loader_query: load failed: %s", t.error.c_str());
+  const hipError_t e = hipEventQuery(t.done);
+  if (e == hipErrorNotReady) return SH_ERR_NOT_READY;
+  SH_HIP(e);
+  return SH_OK;
+}
+
+extern "C" int sh_loader_stream_wait(sh_loader* L, uint64_t ticket, void* stream) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_stream_wait: loader is NULL");
+  std::unique_lock<std::mutex> lk(L->mu);
+  Ticket* t = nullptr;
+  if (int st = wait_issued(L, ticket, lk, &t, "sh_loader_stream_wait")) return st;
+  SH_HIP(hipStreamWaitEvent((hipStream_t)stream, t->done, 0));
+  return SH_OK;
+}
+
+extern "C" int sh_loader_sync(sh_loader* L, uint64_t ticket) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_sync: loader is NULL");
+  hipEvent_t done = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L->mu);
+    Ticket* t = nullptr;
+    if (int st = wait_issued(L, ticket, lk, &t, "sh_loader_sync")) return st;
+    done = t->done;
+  }
+  SH_HIP(hipEventSynchronize(done));
+  return SH_OK;
+}
+
+extern "C" int sh_loader_release(sh_loader* L, uint64_t ticket) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_release: loader is NULL");
+  std::unique_lock<std::mutex> lk(L->mu);
+  auto it = L->tickets.find(ticket);
+  if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "sh_loader_release: unknown ticket %llu", (unsigned long long)ticket);
+  // Never recycle events the worker may still record: wait until it is done with the ticket.
+  L->issued_cv.wait(lk, [&] { return it->second.state != TicketState::Queued; });
+  const bool issued = it->second.state == TicketState::Issued;
+  hipEvent_t copied = it->second.copied, done = it->second.done;
+  lk.unlock();
+  // Events go back to the spare list only once the device has passed them.
+  hipError_t e = issued ? hipEventSynchronize(done) : hipSuccess;
+  if (e == hipSuccess && !issued) e = hipEventSynchronize(copied);
+  lk.lock();
+  it = L->tickets.find(ticket);
+  if (it != L->tickets.end()) {
+    give_events(L, it->second);
+    L->tickets.erase(it);
+  }
+  if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "sh_loader_release: HIP error %d", (int)e);
+  return SH_OK;
+}

@@ -1,0 +1,777 @@
+"""Block scheduler: prefetch window, eviction and the block load path.
+
+Control decisions are those of src/stagehand/scheduler.py — the static
+lookahead policy (:65-142), ``before_block``/``after_block`` (:773-850), the
+prefetch window (:854-883), the load state walk (:885-951), eviction scoring
+and protection (:1128-1182) and the eviction branches (:1184-1375) — and the
+telemetry counters are incremented at the same points. What changed is the
+load itself, on a GPU:
+
+* a block's parameters are described as source pieces + an unpack plan
+  (``stagehand_amd.staging``) instead of being cast / dequantised on the host;
+* the native loader stages, copies and unpacks on its own thread and streams
+  (``AsyncTransferEngine.submit_block_load``);
+* ``before_block`` orders the compute stream after the load on the device
+  (``wait_device``) instead of blocking the host in ``event.synchronize()``;
+* module-backed blocks (the reference's synchronous pageable copy on the
+  compute stream, :1033-1087) go through the same pinned-slab loader; the
+  block is marked GPU_READY at once, as in the reference, and the compute
+  stream waits for the data when the block is first used.
+
+Without a GPU the scheduler runs the reference's CPU behaviour (host copies
+and casts into CPU tensors); SquareQ dequantisation exists only on the device.
+"""
+from __future__ import annotations
+
+import logging
+import mmap
+import os
+import time
+import warnings
+from pathlib import Path
+from typing import TYPE_CHECKING, Any, Protocol
+
+import torch
+from torch import nn
+
+from stagehand_amd.residency import BlockState
+from stagehand_amd.staging import PlanCache, SourceBuilder, squareq_weight_tensors
+
+if TYPE_CHECKING:
+    from stagehand_amd.config import StagehandConfig
+    from stagehand_amd.registry import BlockEntry, BlockRegistry, FileParamSpec
+    from stagehand_amd.residency import ResidencyEntry, ResidencyMap
+    from stagehand_amd.telemetry import StagehandTelemetry
+    from stagehand_amd.transfer import AsyncTransferEngine, TransferHandle
+
+__all__ = ["StaticLookaheadPolicy", "StagehandScheduler", "BudgetLike", "GuardsLike"]
+
+log = logging.getLogger(__name__)
+_STALL_LOGS_ENABLED = str(os.getenv("SERENITY_STAGEHAND_STALL_LOGS", "0")).strip().lower() in {"1", "true", "yes", "on"}
+
+Layout = list[tuple[str, tuple[int, ...], torch.dtype, int, int]]
+
+
+class BudgetLike(Protocol):
+    def above_high_watermark(self) -> bool: ...
+    def below_low_watermark(self) -> bool: ...
+
+
+class GuardsLike(Protocol):
+    def check_output(self, tensor: torch.Tensor, block_id: str, step: int) -> tuple[int, int]: ...
+
+
+# ── policy ───────────────────────────────────────────────────────────────
+
+
+class StaticLookaheadPolicy:
+    """Prefetch the next ``prefetch_window`` blocks; evict by next-use distance × size."""
+
+    def __init__(self, prefetch_window: int = 3, eviction_cooldown_steps: int = 2) -> None:
+        self.prefetch_window = prefetch_window
+        self.eviction_cooldown_steps = eviction_cooldown_steps
+
+    def blocks_to_prefetch(self, cursor: int, total_blocks: int, residency_states: dict[str, str]) -> list[int]:
+        return [cursor + k for k in range(1, self.prefetch_window + 1) if cursor + k < total_blocks]
+
+    def score_for_eviction(self, block_id: str, current_cursor: int, entry_exec_order: int, total_blocks: int,
+                           size_bytes: int) -> float:
+        distance = (entry_exec_order - current_cursor) % total_blocks
+        if distance == 0:
+            distance = total_blocks  # just used / about to be used: farthest in wrap-around order
+        return float(distance * size_bytes)
+
+    def should_evict(self, last_used_step: int, current_step: int) -> bool:
+        return current_step - last_used_step > self.eviction_cooldown_steps
+
+
+# ── layout helpers (src/stagehand/scheduler.py:148-165, 328-346, 396-423) ──
+
+
+def _build_param_layout(module: nn.Module, dtype: torch.dtype) -> Layout:
+    layout: Layout = []
+    offset = 0
+    for name, param in module.named_parameters():
+        numel = param.numel()
+        layout.append((name, tuple(param.shape), dtype, offset, numel))
+        offset += numel * dtype.itemsize
+    return layout
+
+
+def _get_param_data(module: nn.Module, dotted_name: str) -> torch.Tensor:
+    owner = module
+    parts = dotted_name.split(".")
+    for part in parts[:-1]:
+        owner = getattr(owner, part)
+    return getattr(owner, parts[-1]).data
+
+
+def _set_param_data(module: nn.Module, dotted_name: str, data: torch.Tensor) -> None:
+    owner = module
+    parts = dotted_name.split(".")
+    for part in parts[:-1]:
+        owner = getattr(owner, part)
+    param = getattr(owner, parts[-1])
+    try:
+        param.data = data
+    except RuntimeError:
+        setattr(owner, parts[-1], nn.Parameter(data, requires_grad=param.requires_grad))
+
+
+def _restore_params_from_tensor(module: nn.Module, flat_tensor: torch.Tensor, layout: Layout) -> None:
+    """Point every parameter's ``.data`` at its view of the contiguous buffer."""
+    flat = flat_tensor.view(torch.uint8) if flat_tensor.dtype != torch.uint8 else flat_tensor
+    for name, shape, dtype, offset, numel in layout:
+        nbytes = numel * dtype.itemsize
+        _set_param_data(module, name, flat[offset:offset + nbytes].view(dtype).reshape(shape))
+
+
+def _detach_params(module: nn.Module, layout: Layout) -> None:
+    for name, _shape, dtype, _off, _numel in layout:
+        _set_param_data(module, name, torch.empty(0, dtype=dtype))
+
+
+def _flatten_params_into_buffer(module: nn.Module, buffer: torch.Tensor, layout: Layout) -> None:
+    """Host path (no GPU): ``region.copy_(param.to(dtype))`` per parameter (src/stagehand/scheduler.py:168-181)."""
+    params = dict(module.named_parameters())
+    for name, _shape, dtype, offset, numel in layout:
+        region = buffer[offset:offset + numel * dtype.itemsize].view(dtype)
+        region.copy_(params[name].data.to(dtype).reshape(-1))
+
+
+# ── scheduler ────────────────────────────────────────────────────────────
+
+
+class StagehandScheduler:
+    def __init__(
+        self,
+        registry: BlockRegistry,
+        residency: ResidencyMap,
+        transfer_engine: AsyncTransferEngine,
+        budget: BudgetLike,
+        policy: StaticLookaheadPolicy,
+        guards: GuardsLike | None,
+        telemetry: StagehandTelemetry,
+        config: StagehandConfig,
+        inference_mode: bool = False,
+    ) -> None:
+        self._registry = registry
+        self._residency = residency
+        self._engine = transfer_engine
+        self._budget = budget
+        self._policy = policy
+        self._guards = guards
+        self._telemetry = telemetry
+        self._config = config
+        self._inference_mode = inference_mode
+        self._has_cuda = torch.cuda.is_available()
+        self._device = "cuda" if self._has_cuda else "cpu"
+
+        self._current_step = 0
+        self._cursor = 0
+        self._backward_phase = False
+        self._defer_backward_eviction = False
+        self._ordered_blocks: list[BlockEntry] = []
+        self._total_blocks = 0
+        self._order_to_id: dict[int, str] = {}
+        self.refresh_registry_snapshot()
+
+        self._pending_handles: dict[str, TransferHandle] = {}
+        self._conductor_adapter = None
+        self._squareq_adapter = None
+        self._eriquant_adapter = None
+        self._file_maps: dict[str, tuple[Any, mmap.mmap, memoryview]] = {}
+        self._file_tensor_views: dict[tuple, torch.Tensor] = {}
+        self._squareq_layers: dict[str, dict[str, Any]] = {}
+        self._module_param_caches: dict[str, dict[str, torch.Tensor]] = {}
+        self._plans = PlanCache()
+
+    # ── step lifecycle ───────────────────────────────────────────────
+
+    def refresh_registry_snapshot(self) -> None:
+        self._ordered_blocks = self._registry.blocks_in_order()
+        self._total_blocks = len(self._ordered_blocks)
+        self._order_to_id = {e.exec_order: e.block_id for e in self._ordered_blocks}
+
+    def begin_step(self, step: int) -> None:
+        self._current_step = step
+        self._cursor = 0
+        self._backward_phase = False
+        self._telemetry.begin_step(step)
+
+    def end_step(self) -> None:
+        self._backward_phase = False
+        self._engine.reap()
+        self._reconcile_file_backed_grads()
+        self._telemetry.end_step()
+
+    def enter_backward_phase(self) -> None:
+        self._backward_phase = True
+
+    def exit_backward_phase(self) -> None:
+        self._backward_phase = False
+
+    def set_defer_backward_eviction(self, enabled: bool) -> None:
+        self._defer_backward_eviction = enabled
+
+    def _reconcile_file_backed_grads(self) -> None:
+        for entry in self._ordered_blocks:
+            if not entry.file_backed:
+                continue
+            module = entry.module_ref()
+            mutable = set(entry.module_param_names)
+            if module is None or not mutable:
+                continue
+            for name, param in module.named_parameters():
+                if name in mutable and param.device.type == "cpu" and param.grad is not None \
+                        and param.grad.device.type != "cpu":
+                    param.grad = param.grad.to("cpu", non_blocking=True)
+
+    # ── sources ──────────────────────────────────────────────────────
+
+    def _get_file_view(self, source_path: str) -> memoryview:
+        key = str(Path(source_path).expanduser())
+        hit = self._file_maps.get(key)
+        if hit is not None:
+            return hit[2]
+        fh = Path(key).open("rb")
+        mm = mmap.mmap(fh.fileno(), length=0, access=mmap.ACCESS_READ)
+        view = memoryview(mm)
+        self._file_maps[key] = (fh, mm, view)
+        return view
+
+    def _get_file_tensor_view(self, source_path: str, spec: FileParamSpec, file_view: memoryview | None = None) -> torch.Tensor:
+        path = str(Path(source_path).expanduser())
+        key = (path, int(spec.file_offset), int(spec.source_nbytes), spec.source_dtype, spec.source_shape)
+        hit = self._file_tensor_views.get(key)
+        if hit is not None:
+            return hit
+        view = file_view if file_view is not None else self._get_file_view(path)
+        region = view[int(spec.file_offset):int(spec.file_offset) + int(spec.source_nbytes)]
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore", UserWarning)  # read-only mmap: never written through
+            t = torch.frombuffer(region, dtype=spec.source_dtype).reshape(spec.source_shape)
+        self._file_tensor_views[key] = t
+        return t
+
+    def _get_squareq_layers(self, source_path: str) -> dict[str, Any]:
+        key = str(Path(source_path).expanduser())
+        hit = self._squareq_layers.get(key)
+        if hit is not None:
+            return hit
+        payload = torch.load(key, map_location="cpu", weights_only=True, mmap=True)
+        if not isinstance(payload, dict):
+            raise ValueError(f"Invalid SquareQ slab payload at {key}")
+        layers = payload.get("layers")
+        if not isinstance(layers, dict):
+            raise ValueError(f"SquareQ slab missing 'layers' map at {key}")
+        self._squareq_layers[key] = layers
+        return layers
+
+    def _get_squareq_v2_layers(self, source_path: str) -> dict[str, Any]:
+        """V2: safetensors slab + ``<stem>.manifest.json``; tensors are zero-copy views of the mapped file."""
+        from stagehand_amd.squareq_v2 import read_v2_layers
+
+        key = str(Path(source_path).expanduser())
+        hit = self._squareq_layers.get(key)
+        if hit is not None:
+            return hit
+        layers = read_v2_layers(key, str(Path(key).with_suffix(".manifest.json")), self._get_file_view(key))
+        self._squareq_layers[key] = layers
+        return layers
+
+    def close(self) -> None:
+        self._file_tensor_views.clear()
+        for fh, mm, view in self._file_maps.values():
+            for fn in (view.release, mm.close, fh.close):
+                try:
+                    fn()
+                except Exception:
+                    pass
+        self._file_maps.clear()
+        self._squareq_layers.clear()
+        self._module_param_caches.clear()
+        self._plans.clear()
+
+    # ── external bandwidth adapters (not part of this build's path) ──
+
+    def set_conductor_adapter(self, adapter: Any) -> None:
+        self._conductor_adapter = adapter
+
+    def set_squareq_adapter(self, adapter: Any) -> None:
+        self._squareq_adapter = adapter
+
+    def set_eriquant_adapter(self, adapter: Any) -> None:
+        self._eriquant_adapter = adapter
+
+    # ── per-block hooks ──────────────────────────────────────────────
+
+    def before_block(self, block_id: str) -> None:
+        state = self._residency.get_state(block_id)
+        if state == BlockState.GPU_READY:
+            self._telemetry.record_prefetch_hit()
+            self._await_pending_load(block_id)
+        elif state == BlockState.PREFETCHING:
+            t0 = time.monotonic()
+            self._complete_prefetch(block_id)
+            stall_ms = (time.monotonic() - t0) * 1000.0
+            self._telemetry.record_stall(stall_ms)
+            self._telemetry.record_prefetch_miss()
+            log.debug("Stall on block %s: %.2f ms", block_id, stall_ms)
+        else:
+            t0 = time.monotonic()
+            self._load_block_to_gpu(block_id)
+            if self._residency.get_state(block_id) == BlockState.PREFETCHING:
+                self._complete_prefetch(block_id)
+            else:
+                self._await_pending_load(block_id)
+            stall_ms = (time.monotonic() - t0) * 1000.0
+            self._telemetry.record_stall(stall_ms)
+            self._telemetry.record_prefetch_miss()
+            if _STALL_LOGS_ENABLED:
+                log.warning("Hard stall on block %s (was %s): %.2f ms", block_id, state.value, stall_ms)
+
+        self._residency.increment_ref(block_id)
+        self._residency.get_entry(block_id).last_used_step = self._current_step
+        self._cursor += 1
+        if self._budget.above_high_watermark():
+            self._run_eviction(ignore_cooldown=True)
+        self._prefetch_ahead()
+        if self._budget.above_high_watermark():
+            self._run_eviction(ignore_cooldown=True)
+
+    def after_block(self, block_id: str, output: torch.Tensor | None = None) -> None:
+        self._residency.decrement_ref(block_id)
+        self._residency.get_entry(block_id).last_used_step = self._current_step
+        if self._guards is not None and output is not None and self._config.nan_inf_check:
+            nan_count, inf_count = self._guards.check_output(output, block_id, self._current_step)
+            if nan_count > 0 or inf_count > 0:
+                self._telemetry.record_nan_inf(nan_count, inf_count)
+        if self._budget.above_high_watermark() and not (self._backward_phase and self._defer_backward_eviction):
+            self._run_eviction(ignore_cooldown=True)
+
+    def _complete_prefetch(self, block_id: str) -> None:
+        """PREFETCHING → GPU_READY: order the compute stream after the load, restore views."""
+        handle = self._pending_handles.pop(block_id, None)
+        if handle is not None:
+            self._engine.wait_device(handle)
+            self._residency.get_entry(block_id).load = None
+        self._finalize_gpu_load(block_id)
+
+    def _await_pending_load(self, block_id: str) -> None:
+        entry = self._residency.get_entry(block_id)
+        if entry.load is not None:
+            self._engine.wait_device(entry.load)
+            entry.load = None
+
+    # ── prefetch ─────────────────────────────────────────────────────
+
+    def _prefetch_ahead(self) -> None:
+        states: dict[str, str] = {}
+        if type(self._policy) is not StaticLookaheadPolicy:  # the built-in policy never reads the state map
+            states = {e.block_id: self._residency.get_state(e.block_id).value for e in self._ordered_blocks}
+        for idx in self._policy.blocks_to_prefetch(self._cursor - 1, self._total_blocks, states):
+            if idx >= self._total_blocks:
+                break
+            block_id = self._ordered_blocks[idx].block_id
+            if self._residency.get_state(block_id) in (BlockState.GPU_READY, BlockState.PREFETCHING):
+                continue
+            if not self._budget.can_prefetch():
+                break
+            self._load_block_to_gpu(block_id, speculative=True)
+
+    def _load_block_to_gpu(self, block_id: str, speculative: bool = False) -> None:
+        state = self._residency.get_state(block_id)
+        if state in (BlockState.GPU_READY, BlockState.PREFETCHING):
+            return
+        block_entry = self._registry.get(block_id)
+        res_entry = self._residency.get_entry(block_id)
+
+        if block_entry.eriquant_backed:
+            if self._eriquant_adapter is None:
+                log.error("Block %r is eriquant-backed but no adapter set — skipping", block_id)
+                return
+            if state == BlockState.UNLOADED:
+                self._eriquant_adapter.on_prefetch(block_id, self._device)
+                for s in (BlockState.HOST_STAGED, BlockState.PREFETCHING, BlockState.GPU_READY):
+                    self._residency.transition(block_id, s)
+                self._telemetry.record_h2d(block_entry.size_bytes)
+            return
+
+        module_backed = not block_entry.file_backed and not block_entry.squareq_backed
+        if module_backed and state == BlockState.UNLOADED:
+            self._load_module_backed_direct(block_id, block_entry, res_entry)
+            return
+
+        if state == BlockState.UNLOADED:
+            res_entry.host_slab = self._stage_block_to_host(block_entry, res_entry)
+            state = self._residency.get_state(block_id)
+
+        if state == BlockState.HOST_STAGED:
+            if res_entry.gpu_tensor is None:
+                numel = block_entry.size_bytes // block_entry.dtype.itemsize
+                res_entry.gpu_tensor = torch.empty(numel, dtype=block_entry.dtype, device=self._device)
+            staged = res_entry.host_slab
+            if self._has_cuda:
+                handle = self._engine.submit_block_load(block_id, staged, res_entry.gpu_tensor.view(torch.uint8))
+                res_entry.host_slab = None  # the loader owns slab staging and release
+            else:
+                handle = self._engine.submit_h2d(block_id, staged, res_entry.gpu_tensor)
+            self._pending_handles[block_id] = handle
+            self._residency.transition(block_id, BlockState.PREFETCHING)
+            self._telemetry.record_h2d(block_entry.size_bytes)
+
+    def _stage_block_to_host(self, block_entry: BlockEntry, res_entry: ResidencyEntry):
+        """UNLOADED → HOST_STAGED. On a GPU: returns the block's BlockSource (the
+        loader fills a pinned slab from it). Without one: a filled pool slab,
+        as in src/stagehand/scheduler.py:953-1031."""
+        module = block_entry.module_ref()
+        if module is None:
+            res_entry.param_layout = None
+            staged = self._zero_source(block_entry)
+        elif block_entry.squareq_backed or block_entry.file_backed:
+            layout = list(block_entry.param_layout)
+            res_entry.param_layout = layout
+            staged = self._build_source(block_entry, module, layout)
+        elif any(True for _ in module.parameters()):
+            layout = _build_param_layout(module, block_entry.dtype)
+            res_entry.param_layout = layout
+            staged = self._build_module_source(block_entry, module, layout)
+        else:
+            res_entry.param_layout = None
+            staged = self._zero_source(block_entry)
+        self._residency.transition(block_entry.block_id, BlockState.HOST_STAGED)
+        return staged
+
+    # ── source building ──────────────────────────────────────────────
+
+    def _zero_source(self, block_entry: BlockEntry):
+        if self._has_cuda:
+            b = SourceBuilder(block_entry.dtype, block_entry.size_bytes)
+            b.add_zero(0, block_entry.size_bytes)
+            return b.finish()[0]
+        slab = self._engine._pool.acquire(block_entry.size_bytes)
+        slab.buffer[:] = 0
+        return slab
+
+    def _finish_source(self, block_id: str, builder: SourceBuilder):
+        source, descs = builder.finish()
+        if descs is not None:
+            source.plan = self._plans.get(block_id, descs)
+        return source
+
+    def _build_module_source(self, block_entry: BlockEntry, module: nn.Module, layout: Layout):
+        if not self._has_cuda:
+            slab = self._engine._pool.acquire(block_entry.size_bytes)
+            _flatten_params_into_buffer(module, slab.buffer, layout)
+            return slab
+        params = dict(module.named_parameters())
+        b = SourceBuilder(block_entry.dtype, block_entry.size_bytes)
+        for name, _shape, _dtype, offset, _numel in layout:
+            b.add_param(offset, params[name].data)
+        return self._finish_source(block_entry.block_id, b)
+
+    def _build_source(self, block_entry: BlockEntry, module: nn.Module, layout: Layout):
+        if not self._has_cuda:
+            if block_entry.squareq_backed:
+                raise RuntimeError(
+                    f"block {block_entry.block_id!r} is SquareQ-backed: its dequantisation runs on the GPU only")
+            slab = self._engine._pool.acquire(block_entry.size_bytes)
+            self._fill_file_backed_host(block_entry, module, layout, slab.buffer)
+            return slab
+        builder = SourceBuilder(block_entry.dtype, block_entry.size_bytes)
+        if block_entry.squareq_backed:
+            self._add_squareq_regions(block_entry, module, layout, builder)
+        else:
+            self._add_file_regions(block_entry, module, layout, builder)
+        return self._finish_source(block_entry.block_id, builder)
+
+    def _module_value(self, block_id: str, params: dict, name: str, numel: int,
+                      cache: dict[str, torch.Tensor] | None) -> torch.Tensor | None:
+        param = params.get(name)
+        if param is not None and param.data.numel() == numel:
+            if cache is not None and name not in cache:
+                cache[name] = param.data.detach().cpu()
+            return param.data
+        if cache is not None and name in cache:
+            return cache[name]
+        return None
+
+    def _add_file_regions(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, b: SourceBuilder) -> None:
+        """Safetensors-backed block (src/stagehand/scheduler.py:184-241)."""
+        params = dict(module.named_parameters())
+        specs = {s.param_name: s for s in block_entry.file_param_specs}
+        mutable = set(block_entry.module_param_names)
+        sharded = block_entry.source_format == "safetensors_sharded"
+        base_view = None if sharded else self._get_file_view(str(block_entry.source_path))
+        for name, _shape, dtype, offset, numel in layout:
+            spec = specs.get(name)
+            if spec is not None:
+                path = spec.file_path if (spec.file_path and sharded) else str(block_entry.source_path)
+                view = self._get_file_view(path) if (spec.file_path and sharded) else base_view
+                b.add_param(offset, self._get_file_tensor_view(path, spec, view))
+                continue
+            if name in mutable and name in params and params[name].data.numel() == numel:
+                b.add_param(offset, params[name].data)
+                continue
+            b.add_zero(offset, numel * dtype.itemsize)
+
+    def _fill_file_backed_host(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, buffer: torch.Tensor) -> None:
+        params = dict(module.named_parameters())
+        specs = {s.param_name: s for s in block_entry.file_param_specs}
+        mutable = set(block_entry.module_param_names)
+        sharded = block_entry.source_format == "safetensors_sharded"
+        for name, _shape, dtype, offset, numel in layout:
+            region = buffer[offset:offset + numel * dtype.itemsize]
+            spec = specs.get(name)
+            if spec is not None:
+                path = spec.file_path if (spec.file_path and sharded) else str(block_entry.source_path)
+                region.view(dtype).copy_(self._get_file_tensor_view(path, spec).reshape(-1))
+            elif name in mutable and name in params and params[name].data.numel() == numel:
+                region.view(dtype).copy_(params[name].data.to(dtype).reshape(-1))
+            else:
+                region.zero_()
+
+    def _add_squareq_regions(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, b: SourceBuilder) -> None:
+        """SquareQ-backed block: branch structure of src/stagehand/scheduler.py:243-325."""
+        params = dict(module.named_parameters())
+        specs = {s.param_name: s for s in block_entry.squareq_param_specs}
+        mutable = set(block_entry.module_param_names)
+        if block_entry.source_format == "squareq_v2":
+            layers = self._get_squareq_v2_layers(str(block_entry.source_path))
+        else:
+            layers = self._get_squareq_layers(str(block_entry.source_path))
+        cache = self._module_param_caches.setdefault(block_entry.block_id, {})
+        for name, shape, dtype, offset, numel in layout:
+            nbytes = numel * dtype.itemsize
+            spec = specs.get(name)
+            if spec is not None:
+                layer = layers.get(spec.layer_name)
+                if isinstance(layer, dict):
+                    if spec.kind == "weight":
+                        tensors = squareq_weight_tensors(layer)
+                        if tensors is not None:
+                            q, s, z = tensors
+                            out_dim = int(shape[0]) if len(shape) else 0
+                            in_flat = numel // max(out_dim, 1) if out_dim else 0
+                            if len(shape) == 0 or out_dim <= 0 or in_flat <= 0:
+                                b.add_zero(offset, nbytes)
+                                continue
+                            q2d = q.reshape(int(q.shape[0]), -1)
+                            sv, zv = s.reshape(-1), z.reshape(-1)
+                            if sv[:out_dim].numel() != out_dim or zv[:out_dim].numel() != out_dim:
+                                b.add_zero(offset, nbytes)
+                                continue
+                            if q2d.shape[0] < out_dim or q2d.shape[1] < in_flat:
+                                raise ValueError(f"SquareQ layer {spec.layer_name!r}: qweight {tuple(q.shape)} "
+                                                 f"is smaller than {out_dim}x{in_flat}")
+                            b.add_dequant(offset, q2d[:out_dim], in_flat, sv, zv)
+                            continue
+                    elif spec.kind == "bias":
+                        bias = layer.get("bias")
+                        if isinstance(bias, torch.Tensor):
+                            b.add_param(offset, bias)
+                        else:
+                            b.add_zero(offset, nbytes)
+                        continue
+            if name in mutable and name in params:
+                value = self._module_value(block_entry.block_id, params, name, numel, cache)
+                if value is not None:
+                    b.add_param(offset, value)
+                    continue
+            b.add_zero(offset, nbytes)
+
+    # ── module-backed direct load ────────────────────────────────────
+
+    def _load_module_backed_direct(self, block_id: str, block_entry: BlockEntry, res_entry: ResidencyEntry) -> None:
+        """Module-backed block → one contiguous device buffer (src/stagehand/scheduler.py:1033-1087).
+
+        On a GPU the bytes go through a pinned slab on the loader's copy stream
+        (fp32 parameters are rounded to bf16 on the device) and the compute
+        stream waits for them when the block is first used; the FSM walks
+        UNLOADED → HOST_STAGED → PREFETCHING → GPU_READY at once, as in the reference.
+        """
+        module = block_entry.module_ref()
+        if module is None:
+            return
+        layout = _build_param_layout(module, block_entry.dtype)
+        res_entry.param_layout = layout
+        numel = block_entry.size_bytes // block_entry.dtype.itemsize
+        gpu_tensor = torch.empty(numel, dtype=block_entry.dtype, device=self._device)
+        res_entry.gpu_tensor = gpu_tensor
+        gpu_bytes = gpu_tensor.view(torch.uint8)
+        if self._has_cuda:
+            source = self._build_module_source(block_entry, module, layout)
+            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes)
+        else:
+            _flatten_params_into_buffer(module, gpu_bytes, layout)
+        _restore_params_from_tensor(module, gpu_bytes, layout)
+        for param in module.parameters():
+            if param.grad is not None and param.grad.device.type != gpu_tensor.device.type:
+                param.grad = param.grad.to(gpu_tensor.device, non_blocking=True)
+        for s in (BlockState.HOST_STAGED, BlockState.PREFETCHING, BlockState.GPU_READY):
+            self._residency.transition(block_id, s)
+        self._telemetry.record_h2d(block_entry.size_bytes)
+
+    def _finalize_gpu_load(self, block_id: str) -> None:
+        self._residency.transition(block_id, BlockState.GPU_READY)
+        block_entry = self._registry.get(block_id)
+        res_entry = self._residency.get_entry(block_id)
+        if res_entry.param_layout is not None and res_entry.gpu_tensor is not None:
+            module = block_entry.module_ref()
+            if module is not None:
+                gpu_bytes = res_entry.gpu_tensor.view(torch.uint8)
+                _restore_params_from_tensor(module, gpu_bytes, res_entry.param_layout)
+                dev = res_entry.gpu_tensor.device
+                for param in module.parameters():
+                    if param.grad is not None and param.grad.device != dev:
+                        param.grad = param.grad.to(dev, non_blocking=True)
+        if res_entry.host_slab is not None and not hasattr(res_entry.host_slab, "pieces"):
+            self._engine._pool.release(res_entry.host_slab)
+        res_entry.host_slab = None
+
+    # ── eviction ─────────────────────────────────────────────────────
+
+    def _run_eviction(self, ignore_cooldown: bool = False) -> None:
+        cooldown = 0 if ignore_cooldown else self._policy.eviction_cooldown_steps
+        candidates = self._residency.eviction_candidates(current_step=self._current_step, cooldown_steps=cooldown)
+        protected: set[str] = set()
+        base = max(self._cursor - 1, 0)
+        for k in range(1, self._policy.prefetch_window + 1):
+            if base + k < self._total_blocks:
+                protected.add(self._ordered_blocks[base + k].block_id)
+        scored: list[tuple[float, str]] = []
+        for bid, _entry in candidates:
+            if bid in protected:
+                continue
+            be = self._registry.get(bid)
+            scored.append((self._policy.score_for_eviction(bid, self._cursor, be.exec_order, self._total_blocks,
+                                                           be.size_bytes), bid))
+        scored.sort(reverse=True)
+        for _score, bid in scored:
+            if self._budget.below_low_watermark():
+                break
+            self._evict_block(bid, save_back=not self._inference_mode)
+            self._telemetry.record_eviction()
+
+    def _release_device_buffer(self, res_entry: ResidencyEntry) -> None:
+        """Drop the block's device buffer; an unfinished load is waited for on the device first."""
+        if res_entry.load is not None:
+            self._engine.wait_device(res_entry.load)
+            res_entry.load = None
+        res_entry.gpu_tensor = None
+        if res_entry.host_slab is not None and not hasattr(res_entry.host_slab, "pieces"):
+            self._engine._pool.release(res_entry.host_slab)
+        res_entry.host_slab = None
+
+    def _evict_block(self, block_id: str, save_back: bool = False) -> None:
+        block_entry = self._registry.get(block_id)
+        res_entry = self._residency.get_entry(block_id)
+        module = block_entry.module_ref()
+
+        if block_entry.eriquant_backed:
+            if self._eriquant_adapter is None:
+                log.error("Block %r is eriquant-backed but no adapter set — skipping evict", block_id)
+                return
+            self._residency.transition(block_id, BlockState.EVICTING)
+            self._eriquant_adapter.on_offload(block_id, "cpu")
+            self._release_device_buffer(res_entry)
+            res_entry.param_layout = None
+            self._residency.transition(block_id, BlockState.UNLOADED)
+            return
+
+        module_backed = not block_entry.file_backed and not block_entry.squareq_backed
+        if save_back:
+            if module_backed:
+                self._residency.transition(block_id, BlockState.EVICTING)
+                self._await_pending_load(block_id)
+                if module is not None:
+                    for param in module.parameters():
+                        if param.data.device.type != "cpu":
+                            param.data = param.data.to("cpu").clone()
+                        if param.grad is not None and param.grad.device.type != "cpu":
+                            param.grad = param.grad.to("cpu")
+                self._release_device_buffer(res_entry)
+                res_entry.param_layout = None
+                self._residency.transition(block_id, BlockState.UNLOADED)
+                return
+
+            if block_entry.file_backed:
+                self._residency.transition(block_id, BlockState.EVICTING)
+                mutable = set(block_entry.module_param_names)
+                keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
+                specs = {s.param_name: s for s in block_entry.file_param_specs}
+                if module is not None and res_entry.param_layout is not None:
+                    for name, _shape, dtype, _off, _numel in res_entry.param_layout:
+                        if name in mutable:
+                            live = _get_param_data(module, name)
+                            _set_param_data(module, name, live.to(live.device if keep_on_gpu else "cpu").clone())
+                        else:
+                            restored = False
+                            if self._backward_phase and self._defer_backward_eviction:
+                                spec = specs.get(name)
+                                if spec is not None:
+                                    restored = self._restore_file_param_to_cpu_view(module, name, spec, dtype, block_entry)
+                            if not restored:
+                                _set_param_data(module, name, torch.empty(0, dtype=dtype))
+                    for name, param in module.named_parameters():
+                        if name in mutable and param.grad is not None and param.grad.device.type != "cpu":
+                            param.grad = param.grad.to("cpu", non_blocking=True)
+                self._release_device_buffer(res_entry)
+                res_entry.param_layout = None
+                self._residency.transition(block_id, BlockState.UNLOADED)
+                return
+
+            # Generic D2H save-back through a temporary slab (src/stagehand/scheduler.py:1279-1331).
+            self._residency.transition(block_id, BlockState.EVICTING)
+            if res_entry.gpu_tensor is not None:
+                self._await_pending_load(block_id)
+                slab = self._engine._pool.acquire(block_entry.size_bytes)
+                handle = self._engine.submit_d2h(block_id, res_entry.gpu_tensor, slab)
+                self._engine.wait(handle)
+                self._telemetry.record_d2h(res_entry.gpu_tensor.numel() * res_entry.gpu_tensor.element_size())
+                if module is not None and res_entry.param_layout is not None:
+                    _restore_params_from_tensor(module, slab.buffer, res_entry.param_layout)
+                    for name, *_rest in res_entry.param_layout:
+                        _set_param_data(module, name, _get_param_data(module, name).clone())
+                self._engine._pool.release(slab)
+                res_entry.host_slab = None
+            if module is not None:
+                for param in module.parameters():
+                    if param.grad is not None and param.grad.device.type != "cpu":
+                        param.grad = param.grad.to("cpu", non_blocking=True)
+            self._release_device_buffer(res_entry)
+            self._residency.transition(block_id, BlockState.UNLOADED)
+            return
+
+        # No save-back: GPU_READY → GPU_FREEING → UNLOADED.
+        self._residency.transition(block_id, BlockState.GPU_FREEING)
+        if module is not None and res_entry.param_layout is not None:
+            if module_backed:
+                self._await_pending_load(block_id)
+                for name, *_rest in res_entry.param_layout:
+                    _set_param_data(module, name, _get_param_data(module, name).to("cpu").clone())
+            elif block_entry.file_backed:  # SquareQ-backed blocks are file-backed too (registry BlockEntry.file_backed)
+                resident = set(block_entry.module_param_names)
+                keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
+                for name, _shape, dtype, _off, _numel in res_entry.param_layout:
+                    if name in resident:
+                        data = _get_param_data(module, name)
+                        _set_param_data(module, name, data.to(data.device if keep_on_gpu else "cpu").clone())
+                    else:
+                        _set_param_data(module, name, torch.empty(0, dtype=dtype))
+            else:
+                _detach_params(module, res_entry.param_layout)
+        self._release_device_buffer(res_entry)
+        res_entry.param_layout = None
+        self._residency.transition(block_id, BlockState.UNLOADED)
+
+    def _restore_file_param_to_cpu_view(self, module: nn.Module, name: str, spec: FileParamSpec, runtime_dtype: torch.dtype,
+                                        block_entry: BlockEntry) -> bool:
+        sharded = block_entry.source_format == "safetensors_sharded"
+        path = spec.file_path if (spec.file_path and sharded) else str(block_entry.source_path)
+        t = self._get_file_tensor_view(path, spec)
+        if spec.source_dtype != runtime_dtype:
+            t = t.to(dtype=runtime_dtype)
+        _set_param_data(module, name, t)
+        return True

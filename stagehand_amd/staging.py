@@ -1,0 +1,193 @@
+"""Block source assembly for the device path.
+
+The reference converts every parameter on the host while copying it into the
+pinned slab (casts at src/stagehand/scheduler.py:181, 224-230, 1066-1071;
+SquareQ dequant at :290-300; zero fill at :240, :276-297, :325) and sends the
+finished runtime-dtype block over PCIe. Here a block is described instead as
+raw source pieces plus an unpack plan:
+
+* same-dtype parameters (bf16 → bf16) are byte copies;
+* fp32 parameters become SH_KIND_F32_BF16 regions, cast on the device;
+* SquareQ weights travel as int8 rows (with the padded row stride of the slab
+  format) plus per-row fp32 scales (and zero points when any is non-zero) and
+  become SH_KIND_I8_ROWSCALE_* regions, dequantised on the device — half the
+  PCIe bytes of a bf16 block;
+* missing parameters become zero-fill regions.
+
+When every region is a byte copy or zero fill, the slab image equals the
+destination image and no kernel runs (``plan is None``: a single H2D copy).
+The branch structure of the SquareQ fallbacks is that of
+src/stagehand/scheduler.py:243-325; ``oracle/squareq.py`` restates it on the
+CPU and the GPU tests compare the two.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Mapping
+
+import numpy as np
+import torch
+
+from stagehand_amd.transfer import BlockSource
+from stagehand_amd.unpack import (
+    KIND_BF16_F32,
+    KIND_COPY_BYTES,
+    KIND_F32_BF16,
+    KIND_I8_ROWSCALE_BF16,
+    KIND_I8_ROWSCALE_F32,
+    KIND_ZERO_BYTES,
+    UnpackPlan,
+    make_descs,
+)
+
+__all__ = ["SourceBuilder", "PlanCache", "SUPPORTED_RUNTIME_DTYPES"]
+
+SUPPORTED_RUNTIME_DTYPES = (torch.bfloat16, torch.float32)
+_ALIGN = 16
+
+
+def _align(x: int) -> int:
+    return (x + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+def _host_contig(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach()
+    if t.device.type != "cpu":
+        t = t.to("cpu")
+    return t.contiguous()
+
+
+_ZERO_HOST = torch.zeros(0, dtype=torch.uint8)
+
+
+def _zeros(nbytes: int) -> torch.Tensor:
+    global _ZERO_HOST
+    if _ZERO_HOST.numel() < nbytes:
+        _ZERO_HOST = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8)
+    return _ZERO_HOST[:nbytes]
+
+
+@dataclass
+class SourceBuilder:
+    """Collects the regions of one block and lays out its source slab."""
+
+    runtime_dtype: torch.dtype
+    dst_bytes: int
+    _regions: list[tuple] = field(default_factory=list)  # (kind, dst_off, host tensor|None, rows, cols, ld, scale rows)
+    _scales: list[torch.Tensor] = field(default_factory=list)
+    _zps: list[torch.Tensor | None] = field(default_factory=list)
+
+    def __post_init__(self) -> None:
+        if self.runtime_dtype not in SUPPORTED_RUNTIME_DTYPES:
+            raise ValueError(f"device path supports runtime dtypes {SUPPORTED_RUNTIME_DTYPES}, got {self.runtime_dtype}")
+
+    # ── regions ──────────────────────────────────────────────────────
+
+    def add_param(self, dst_off: int, value: torch.Tensor) -> None:
+        """``dst ← value.to(runtime_dtype)`` (rounded on the device when narrowing)."""
+        v = _host_contig(value).reshape(-1)
+        rt = self.runtime_dtype
+        if v.dtype == rt:
+            self._regions.append((KIND_COPY_BYTES, dst_off, v.view(torch.uint8), 1, v.numel() * v.element_size(), 0, 0))
+            return
+        if v.dtype == torch.float16:
+            v = v.to(torch.float32)  # exact widening; any rounding happens on the device
+        if rt == torch.bfloat16 and v.dtype == torch.float32:
+            self._regions.append((KIND_F32_BF16, dst_off, v.view(torch.uint8), 1, v.numel(), 0, 0))
+        elif rt == torch.float32 and v.dtype == torch.bfloat16:
+            self._regions.append((KIND_BF16_F32, dst_off, v.view(torch.uint8), 1, v.numel(), 0, 0))
+        elif rt == torch.float32 and v.dtype == torch.float32:
+            self._regions.append((KIND_COPY_BYTES, dst_off, v.view(torch.uint8), 1, v.numel() * 4, 0, 0))
+        else:
+            raise ValueError(f"no device conversion from {v.dtype} to {rt}")
+
+    def add_zero(self, dst_off: int, nbytes: int) -> None:
+        if nbytes > 0:
+            self._regions.append((KIND_ZERO_BYTES, dst_off, None, 1, nbytes, 0, 0))
+
+    def add_dequant(self, dst_off: int, q_rows: torch.Tensor, in_flat: int, scale: torch.Tensor,
+                    zero_point: torch.Tensor | None) -> None:
+        """SquareQ weight: q_rows is the (out, ld) int8 row block, the first in_flat columns are used."""
+        q = _host_contig(q_rows)
+        if q.dtype != torch.int8:
+            raise ValueError(f"SquareQ qweight must be int8, got {q.dtype}")
+        out_dim, ld = int(q.shape[0]), int(q.shape[1])
+        if in_flat > ld:
+            raise ValueError(f"SquareQ row of {ld} values is shorter than in_features {in_flat}")
+        kind = KIND_I8_ROWSCALE_BF16 if self.runtime_dtype == torch.bfloat16 else KIND_I8_ROWSCALE_F32
+        s = _host_contig(scale).reshape(-1)[:out_dim].to(torch.float32)
+        z = None if zero_point is None else _host_contig(zero_point).reshape(-1)[:out_dim].to(torch.float32)
+        self._regions.append((kind, dst_off, q.view(torch.uint8).reshape(-1), out_dim, in_flat, ld, out_dim))
+        self._scales.append(s)
+        self._zps.append(z)
+
+    # ── layout ───────────────────────────────────────────────────────
+
+    def finish(self) -> tuple[BlockSource, np.ndarray | None]:
+        """Returns the block source and, when a kernel is needed, its descriptor table."""
+        if all(r[0] in (KIND_COPY_BYTES, KIND_ZERO_BYTES) for r in self._regions):
+            pieces = []
+            for kind, dst_off, t, _r, nbytes, _ld, _s in self._regions:
+                pieces.append((dst_off, t if kind == KIND_COPY_BYTES else _zeros(nbytes)))
+            return BlockSource(pieces=pieces, src_bytes=self.dst_bytes), None
+
+        pieces: list[tuple[int, torch.Tensor]] = []
+        rows: list[tuple] = []
+        cursor = 0
+        scale_row = 0
+        for kind, dst_off, t, r, c, ld, srows in self._regions:
+            if kind == KIND_ZERO_BYTES:
+                rows.append((kind, 0, dst_off, r, c, 0, 0))
+                continue
+            off = _align(cursor)
+            pieces.append((off, t))
+            cursor = off + t.numel()
+            rows.append((kind, off, dst_off, r, c, ld, scale_row))
+            scale_row += srows
+        scale_off = zp_off = -1
+        if self._scales:
+            scale_off = _align(cursor)
+            scales = torch.cat(self._scales)
+            pieces.append((scale_off, scales.view(torch.uint8)))
+            cursor = scale_off + scales.numel() * 4
+            if any(z is not None and bool(torch.any(z != 0)) for z in self._zps):
+                zp_off = _align(cursor)
+                zps = torch.cat([z if z is not None else torch.zeros_like(s) for z, s in zip(self._zps, self._scales)])
+                pieces.append((zp_off, zps.view(torch.uint8)))
+                cursor = zp_off + zps.numel() * 4
+        src = BlockSource(pieces=pieces, src_bytes=max(cursor, 1), scale_off=scale_off, zp_off=zp_off,
+                          n_scale=scale_row)
+        return src, make_descs(rows)
+
+
+class PlanCache:
+    """Device-resident unpack plans keyed by block; rebuilt when the table changes."""
+
+    def __init__(self) -> None:
+        self._plans: dict[str, tuple[bytes, UnpackPlan]] = {}
+
+    def get(self, block_id: str, descs: np.ndarray) -> UnpackPlan:
+        key = descs.tobytes()
+        hit = self._plans.get(block_id)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        plan = UnpackPlan(descs)
+        if hit is not None:
+            hit[1].close()
+        self._plans[block_id] = (key, plan)
+        return plan
+
+    def clear(self) -> None:
+        for _k, plan in self._plans.values():
+            try:
+                plan.close()
+            except Exception:
+                pass
+        self._plans.clear()
+
+
+def squareq_weight_tensors(layer: Mapping[str, Any]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None:
+    q, s, z = layer.get("qweight"), layer.get("scale"), layer.get("zero_point")
+    if isinstance(q, torch.Tensor) and isinstance(s, torch.Tensor) and isinstance(z, torch.Tensor):
+        return q, s, z
+    return None

@@ -1,0 +1,422 @@
+"""Async H2D/D2H transfers and native block loads.
+
+``AsyncTransferEngine`` keeps the contract of src/stagehand/transfer.py:69-314
+— ``submit_h2d`` / ``submit_d2h`` / ``poll`` / ``wait`` / ``inflight_count`` /
+``reap`` / ``drain`` with ``max_inflight`` backpressure and a
+``TransferHandle`` carrying the same fields — but its copies are
+``hipMemcpyAsync`` calls on a native copy stream fenced by native events
+(include/stagehand_native.h), and it adds the device path the scheduler uses
+for whole blocks:
+
+* ``submit_block_load`` hands a block's source pieces to the native loader
+  (a worker thread: gather into a pinned slab, H2D on the copy stream, unpack
+  kernel on the unpack stream), returning immediately;
+* ``wait_device`` makes the caller's current stream wait for a transfer on the
+  device, without blocking the host (the reference's ``wait`` blocks the host
+  in ``event.synchronize()``, src/stagehand/transfer.py:203; ``wait`` here keeps
+  that behaviour for callers that need it).
+
+Without a GPU, copies are synchronous ``copy_`` calls and handles complete at
+submission, as in the reference (src/stagehand/transfer.py:136-138).
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import TYPE_CHECKING, Any
+
+import numpy as np
+import torch
+
+from stagehand_amd import _native
+from stagehand_amd._native import COPY_ITEM_DTYPE, LOAD_REQUEST_DTYPE
+from stagehand_amd.errors import TransferError
+
+if TYPE_CHECKING:
+    from stagehand_amd.pool import PinnedPool, PinnedSlab
+    from stagehand_amd.unpack import UnpackPlan
+
+__all__ = ["TransferHandle", "AsyncTransferEngine", "NativeEvent", "BlockSource"]
+
+log = logging.getLogger(__name__)
+_STALL_LOGS_ENABLED = str(os.getenv("SERENITY_STAGEHAND_STALL_LOGS", "0")).strip().lower() in {"1", "true", "yes", "on"}
+
+
+class NativeEvent:
+    """A native HIP event with the ``query``/``synchronize`` face of ``torch.cuda.Event``."""
+
+    def __init__(self) -> None:
+        h = ctypes.c_void_p()
+        _native.call("sh_event_create", 0, ctypes.byref(h))
+        self.handle = h
+
+    def record(self, stream_handle: int) -> None:
+        _native.call("sh_event_record", self.handle, stream_handle)
+
+    def query(self) -> bool:
+        return _native.call("sh_event_query", self.handle) == _native.SH_OK
+
+    def synchronize(self) -> None:
+        _native.call("sh_event_sync", self.handle)
+
+    def __del__(self) -> None:
+        try:
+            if self.handle is not None:
+                _native.lib().sh_event_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+@dataclass
+class TransferHandle:
+    """Returned by every submit (fields of src/stagehand/transfer.py:32-42)."""
+
+    handle_id: int
+    block_id: str
+    direction: str  # "h2d", "d2h" or "load"
+    event: Any  # NativeEvent | None
+    submitted_at: float
+    size_bytes: int
+    completed: bool = False
+    ticket: int | None = None
+    keepalive: list = field(default_factory=list, repr=False)
+    device_waited: bool = False
+
+
+@dataclass
+class BlockSource:
+    """What one block load sends: slab pieces (offset, host tensor), the bytes
+    to send, and optionally an unpack plan with the offsets of its scales."""
+
+    pieces: list[tuple[int, torch.Tensor]]
+    src_bytes: int
+    plan: "UnpackPlan | None" = None
+    scale_off: int = -1
+    zp_off: int = -1
+    n_scale: int = 0
+
+
+def _current_stream_handle() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class AsyncTransferEngine:
+    """Copies between pinned slabs and device tensors on a dedicated stream."""
+
+    def __init__(
+        self,
+        pool: PinnedPool,
+        max_inflight: int = 2,
+        copy_stream: torch.cuda.Stream | None = None,
+        copy_threads: int | None = None,
+    ) -> None:
+        self._pool = pool
+        self._max_inflight = max_inflight
+        self._has_cuda = torch.cuda.is_available()
+        self._lock = threading.Lock()
+        self._cond = threading.Condition(self._lock)
+        self._inflight: list[TransferHandle] = []
+        self._next_handle_id = 0
+        self._loader = None
+        self._owned_stream = None
+        self._copy_stream = None
+        self._copy_threads = copy_threads or min(16, os.cpu_count() or 1)
+        if self._has_cuda:
+            _native.call("sh_set_device", torch.cuda.current_device())
+            if copy_stream is not None:
+                self._copy_stream = copy_stream
+            else:
+                h = ctypes.c_void_p()
+                _native.call("sh_stream_create", ctypes.byref(h))
+                self._owned_stream = h
+                self._copy_stream = torch.cuda.ExternalStream(h.value)
+
+    # ── properties ───────────────────────────────────────────────────
+
+    @property
+    def copy_stream(self):
+        return self._copy_stream
+
+    @property
+    def pool(self) -> PinnedPool:
+        return self._pool
+
+    def _loader_handle(self) -> ctypes.c_void_p:
+        if self._loader is None:
+            if self._pool.handle is None:
+                raise RuntimeError("the pinned pool has been shut down")
+            h = ctypes.c_void_p()
+            _native.call("sh_loader_create", self._pool.handle, self._copy_threads, ctypes.byref(h))
+            self._loader = h
+        return self._loader
+
+    def loader_streams(self) -> tuple[int, int]:
+        cs, us = ctypes.c_void_p(), ctypes.c_void_p()
+        _native.call("sh_loader_streams", self._loader_handle(), ctypes.byref(cs), ctypes.byref(us))
+        return cs.value, us.value
+
+    # ── reference-compatible copies ──────────────────────────────────
+
+    def submit_h2d(self, block_id: str, host_slab: PinnedSlab, gpu_dest: torch.Tensor) -> TransferHandle:
+        size = gpu_dest.numel() * gpu_dest.element_size()
+        self._wait_for_slot()
+        handle = self._make_handle(block_id, "h2d", size)
+        if self._has_cuda:
+            if size > host_slab.size_bytes:
+                raise TransferError(f"H2D of {size} bytes from a {host_slab.size_bytes}-byte slab")
+            cs = self._copy_stream.cuda_stream
+            self._fence_copy_stream(cs)
+            self._check_copy(_native.lib().sh_memcpy_h2d_async(gpu_dest.data_ptr(), host_slab.buffer.data_ptr(), size, cs),
+                             block_id, "h2d")
+            handle.event = NativeEvent()
+            handle.event.record(cs)
+            handle.keepalive = [gpu_dest]
+        else:
+            gpu_dest.view(-1).view(torch.uint8).copy_(host_slab.buffer[:size])
+            handle.completed = True
+        with self._lock:
+            self._inflight.append(handle)
+        return handle
+
+    def submit_d2h(self, block_id: str, gpu_src: torch.Tensor, host_slab: PinnedSlab) -> TransferHandle:
+        size = gpu_src.numel() * gpu_src.element_size()
+        self._wait_for_slot()
+        handle = self._make_handle(block_id, "d2h", size)
+        if self._has_cuda:
+            if size > host_slab.size_bytes:
+                raise TransferError(f"D2H of {size} bytes into a {host_slab.size_bytes}-byte slab")
+            cs = self._copy_stream.cuda_stream
+            self._fence_copy_stream(cs)
+            self._check_copy(_native.lib().sh_memcpy_d2h_async(host_slab.buffer.data_ptr(), gpu_src.data_ptr(), size, cs),
+                             block_id, "d2h")
+            handle.event = NativeEvent()
+            handle.event.record(cs)
+            handle.keepalive = [gpu_src]
+        else:
+            host_slab.buffer[:size].copy_(gpu_src.reshape(-1).view(torch.uint8))
+            handle.completed = True
+        with self._lock:
+            self._inflight.append(handle)
+        return handle
+
+    # ── native block loads ───────────────────────────────────────────
+
+    def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor) -> TransferHandle:
+        """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path)."""
+        if not self._has_cuda:
+            raise RuntimeError("submit_block_load needs a GPU")
+        dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
+        self._wait_for_slot()
+        handle = self._make_handle(block_id, "load", source.src_bytes)
+        items = np.zeros(len(source.pieces), dtype=COPY_ITEM_DTYPE)
+        keep: list = [gpu_dest]
+        for i, (off, t) in enumerate(source.pieces):
+            if t.device.type != "cpu" or not t.is_contiguous():
+                raise ValueError(f"block {block_id}: piece {i} must be a contiguous host tensor")
+            items[i] = (off, t.data_ptr(), t.numel() * t.element_size())
+            keep.append(t)
+        keep.append(items)
+        req = np.zeros(1, dtype=LOAD_REQUEST_DTYPE)
+        req[0]["pieces"] = items.ctypes.data
+        req[0]["n_pieces"] = len(items)
+        req[0]["src_bytes"] = source.src_bytes
+        req[0]["dst"] = gpu_dest.data_ptr()
+        req[0]["dst_bytes"] = dst_bytes
+        req[0]["scale_off"] = source.scale_off
+        req[0]["zp_off"] = source.zp_off
+        req[0]["n_scale"] = source.n_scale
+        req[0]["copy_threads"] = self._copy_threads
+        if source.plan is not None:
+            staging = torch.empty(max(source.src_bytes, 1), dtype=torch.uint8, device=gpu_dest.device)
+            keep.append(staging)
+            keep.append(source.plan)
+            req[0]["plan"] = source.plan.handle.value
+            req[0]["staging"] = staging.data_ptr()
+            req[0]["staging_bytes"] = staging.numel()
+        ticket = ctypes.c_uint64()
+        st = _native.lib().sh_loader_submit(self._loader_handle(), req.ctypes.data, _current_stream_handle(),
+                                            ctypes.byref(ticket))
+        if st != _native.SH_OK:
+            self._raise_transfer(st, block_id, "load")
+        handle.ticket = ticket.value
+        handle.keepalive = keep
+        with self._lock:
+            self._inflight.append(handle)
+        return handle
+
+    # ── completion ───────────────────────────────────────────────────
+
+    def poll(self, handle: TransferHandle) -> bool:
+        if handle.completed:
+            return True
+        if handle.ticket is not None:
+            st = _native.lib().sh_loader_query(self._loader, handle.ticket)
+            if st == _native.SH_ERR_NOT_READY:
+                return False
+            if st != _native.SH_OK:
+                self._raise_transfer(st, handle.block_id, handle.direction)
+            self._complete_handle(handle)
+            return True
+        if handle.event is None:
+            if not self._has_cuda:
+                return True
+            return handle.completed
+        done = handle.event.query()
+        if done:
+            self._complete_handle(handle)
+        return done
+
+    def wait_device(self, handle: TransferHandle, stream_handle: int | None = None) -> None:
+        """Make ``stream_handle`` (default: current stream) wait for ``handle`` on the device."""
+        if handle.completed or handle.device_waited:
+            return
+        if not self._has_cuda:
+            self._complete_handle(handle)
+            return
+        sh = _current_stream_handle() if stream_handle is None else stream_handle
+        if handle.ticket is not None:
+            st = _native.lib().sh_loader_stream_wait(self._loader, handle.ticket, sh)
+            if st != _native.SH_OK:
+                self._raise_transfer(st, handle.block_id, handle.direction)
+        elif handle.event is not None:
+            _native.call("sh_stream_wait_event", sh, handle.event.handle)
+        handle.device_waited = True
+
+    def wait(self, handle: TransferHandle) -> None:
+        """Block the host until ``handle`` completes (the reference's wait), and order the current stream after it."""
+        if handle.completed:
+            return
+        if handle.ticket is None and handle.event is None:
+            self._complete_handle(handle)
+            return
+        t0 = time.monotonic()
+        if handle.ticket is not None:
+            st = _native.lib().sh_loader_sync(self._loader, handle.ticket)
+            if st != _native.SH_OK:
+                self._raise_transfer(st, handle.block_id, handle.direction)
+        else:
+            handle.event.synchronize()
+        self.wait_device(handle)
+        elapsed_ms = (time.monotonic() - t0) * 1000.0
+        if _STALL_LOGS_ENABLED and elapsed_ms > 1.0:
+            log.warning("Transfer stall: block=%s dir=%s wait=%.2f ms", handle.block_id, handle.direction, elapsed_ms)
+        self._complete_handle(handle)
+
+    def inflight_count(self) -> int:
+        with self._lock:
+            return len(self._inflight)
+
+    def reap(self) -> int:
+        with self._lock:
+            before = len(self._inflight)
+            self._reap_completed_locked()
+            return before - len(self._inflight)
+
+    def drain(self) -> None:
+        while True:
+            with self._lock:
+                remaining = list(self._inflight)
+            if not remaining:
+                break
+            for h in remaining:
+                self.wait(h)
+
+    def shutdown(self) -> None:
+        try:
+            self.drain()
+        finally:
+            if self._loader is not None:
+                _native.call("sh_loader_destroy", self._loader)
+                self._loader = None
+            if self._owned_stream is not None:
+                _native.call("sh_stream_sync", self._owned_stream)
+                _native.call("sh_stream_destroy", self._owned_stream)
+                self._owned_stream = None
+
+    def __del__(self) -> None:
+        try:
+            if self._loader is not None:
+                _native.lib().sh_loader_destroy(self._loader)
+                self._loader = None
+        except Exception:
+            pass
+
+    # ── internals ────────────────────────────────────────────────────
+
+    def _fence_copy_stream(self, copy_stream_handle: int) -> None:
+        """The copy stream waits for work already queued on the current stream (e.g. the destination's allocation)."""
+        ev = NativeEvent()
+        ev.record(_current_stream_handle())
+        _native.call("sh_stream_wait_event", copy_stream_handle, ev.handle)
+
+    def _check_copy(self, status: int, block_id: str, direction: str) -> None:
+        if status != _native.SH_OK:
+            self._raise_transfer(status, block_id, direction)
+
+    def _raise_transfer(self, status: int, block_id: str, direction: str) -> None:
+        msg = _native.last_error() or f"status {status}"
+        if status == _native.SH_ERR_INVALID:
+            raise ValueError(f"{direction} of block {block_id!r}: {msg}")
+        raise TransferError(f"{direction} of block {block_id!r} failed: {msg}")
+
+    def _make_handle(self, block_id: str, direction: str, size_bytes: int) -> TransferHandle:
+        with self._lock:
+            hid = self._next_handle_id
+            self._next_handle_id += 1
+        return TransferHandle(hid, block_id, direction, None, time.monotonic(), size_bytes)
+
+    def _wait_for_slot(self) -> None:
+        t0 = time.monotonic()
+        warned = False
+        with self._cond:
+            while len(self._inflight) >= self._max_inflight:
+                self._reap_completed_locked()
+                if len(self._inflight) < self._max_inflight:
+                    break
+                self._cond.wait(timeout=0.001)
+                if not warned and (time.monotonic() - t0) * 1000.0 > 1.0:
+                    log.warning("AsyncTransferEngine: backpressure wait %.2f ms", (time.monotonic() - t0) * 1000.0)
+                    warned = True
+
+    def _complete_handle(self, handle: TransferHandle) -> None:
+        if handle.completed:
+            return
+        handle.completed = True
+        if handle.ticket is not None and self._loader is not None:
+            _native.call("sh_loader_release", self._loader, handle.ticket)
+            handle.ticket = None
+        handle.keepalive = []
+        with self._cond:
+            try:
+                self._inflight.remove(handle)
+            except ValueError:
+                pass
+            self._cond.notify_all()
+
+    def _reap_completed_locked(self) -> None:
+        done: list[TransferHandle] = []
+        for h in self._inflight:
+            if h.completed:
+                done.append(h)
+            elif h.ticket is not None:
+                st = _native.lib().sh_loader_query(self._loader, h.ticket)
+                if st == _native.SH_OK:
+                    done.append(h)
+            elif h.event is not None and h.event.query():
+                done.append(h)
+            elif h.event is None and not self._has_cuda:
+                done.append(h)
+        for h in done:
+            h.completed = True
+            if h.ticket is not None and self._loader is not None:
+                _native.lib().sh_loader_release(self._loader, h.ticket)
+                h.ticket = None
+            h.keepalive = []
+            self._inflight.remove(h)
+        if done:
+            self._cond.notify_all()
