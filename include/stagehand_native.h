@@ -258,6 +258,14 @@ typedef struct sh_load_request {
   uint64_t n_scale;
   int32_t copy_threads;  /* host copy threads for this request; <= 0: loader default */
   int32_t reserved;
+  /* Optional pinned host image of the whole source (src_bytes; from
+   * sh_host_alloc). When set, the pieces are gathered into the image (offsets
+   * relative to it; n_pieces may be 0 when it already holds them) and the H2D
+   * reads the image directly, with no pool slab — the turbo engine's
+   * all-blocks-pinned layout (turbo_src/engine.rs:132-138) for sources that do
+   * not change. Before re-gathering into an image the loader waits for the
+   * previous copy out of it. */
+  void* image;
 } sh_load_request;
 
 typedef struct sh_loader sh_loader;
@@ -274,6 +282,13 @@ int sh_loader_stream_wait(sh_loader* loader, uint64_t ticket, void* stream);
 int sh_loader_sync(sh_loader* loader, uint64_t ticket);
 /* Forgets a ticket (waits for its device work first). */
 int sh_loader_release(sh_loader* loader, uint64_t ticket);
+/* Timing of later submissions (no reference counterpart; the per-block copy
+ * and unpack GB/s telemetry): when enabled, each ticket's copy-start,
+ * copy-end and done points are timing events. sh_loader_ticket_times waits for
+ * the ticket and returns the three times in ms after `ref_event` (a timing
+ * event recorded earlier); call it before sh_loader_release. */
+int sh_loader_set_timing(sh_loader* loader, int enable);
+int sh_loader_ticket_times(sh_loader* loader, uint64_t ticket, void* ref_event, float* out3);
 
 /* Host copy of the kernels' row-index division (floor(n[i] / d) through the
  * 64-bit multiplicative inverse stored in sh_unpack_desc.div_magic), exported

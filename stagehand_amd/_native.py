@@ -143,13 +143,15 @@ _SIGNATURES: dict[str, list] = {
     "sh_loader_stream_wait": [_vp, ctypes.c_uint64, _vp],
     "sh_loader_sync": [_vp, ctypes.c_uint64],
     "sh_loader_release": [_vp, ctypes.c_uint64],
+    "sh_loader_set_timing": [_vp, _i32],
+    "sh_loader_ticket_times": [_vp, ctypes.c_uint64, _vp, _vp],
 }
 
 # Mirror of `struct sh_load_request`.
 LOAD_REQUEST_DTYPE = np.dtype([
     ("pieces", "<u8"), ("n_pieces", "<u8"), ("src_bytes", "<u8"), ("plan", "<u8"), ("staging", "<u8"),
     ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
-    ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"),
+    ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"), ("image", "<u8"),
 ])
 
 # Mirror of `struct sh_pool_stats`.

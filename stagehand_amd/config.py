@@ -24,6 +24,10 @@ class StagehandConfig:
     # transfers
     max_inflight_transfers: int = 2
     copy_stream_priority: int = -1
+    # keep each file/SquareQ block's source bytes in a pinned host image after
+    # its first load, so later loads are a single DMA (no staging copy); costs
+    # host memory equal to the streamed bytes of all such blocks
+    pinned_source_cache: bool = False
     # scheduling policy
     policy: str = "static"
     prefetch_window_blocks: int = 3

@@ -50,6 +50,7 @@ struct Ticket {
   hipEvent_t ready = nullptr;   // recorded on the caller's stream at submit
   hipEvent_t copied = nullptr;  // H2D of the slab finished
   hipEvent_t done = nullptr;    // destination fully written
+  hipEvent_t start = nullptr;   // timing only: copy stream reached this load
   int status = SH_OK;
   std::string error;
   // request
@@ -64,6 +65,7 @@ struct Ticket {
   int64_t zp_off = -1;
   uint64_t n_scale = 0;
   int copy_threads = 1;
+  void* image = nullptr;
 };
 
 }  // namespace
@@ -81,8 +83,12 @@ struct sh_loader {
   std::deque<uint64_t> queue;
   std::unordered_map<uint64_t, Ticket> tickets;
   std::vector<hipEvent_t> spare_events;
+  // image → event recorded after the last H2D that read it (worker thread only)
+  std::unordered_map<void*, hipEvent_t> image_fence;
   uint64_t next_ticket = 1;
   bool stop = false;
+  bool timing = false;  // copied/done/start are timing events
+  std::vector<hipEvent_t> spare_timing_events;
   std::thread worker;
 };
 
@@ -91,20 +97,25 @@ extern "C" int sh_unpack(const sh_plan* plan, const void* src, size_t src_bytes,
 
 namespace {
 
-hipError_t take_event(sh_loader* L, hipEvent_t* ev) {
-  if (!L->spare_events.empty()) {
-    *ev = L->spare_events.back();
-    L->spare_events.pop_back();
+hipError_t take_event(sh_loader* L, hipEvent_t* ev, bool timing = false) {
+  std::vector<hipEvent_t>& spares = timing ? L->spare_timing_events : L->spare_events;
+  if (!spares.empty()) {
+    *ev = spares.back();
+    spares.pop_back();
     return hipSuccess;
   }
-  return hipEventCreateWithFlags(ev, hipEventDisableTiming);
+  return hipEventCreateWithFlags(ev, timing ? hipEventDefault : hipEventDisableTiming);
 }
 
 void give_events(sh_loader* L, Ticket& t) {
-  for (hipEvent_t* ev : {&t.ready, &t.copied, &t.done}) {
-    if (*ev) L->spare_events.push_back(*ev);
+  if (t.ready) L->spare_events.push_back(t.ready);
+  const bool timed = t.start != nullptr;
+  for (hipEvent_t* ev : {&t.copied, &t.done}) {
+    if (*ev) (timed ? L->spare_timing_events : L->spare_events).push_back(*ev);
     *ev = nullptr;
   }
+  if (t.start) L->spare_timing_events.push_back(t.start);
+  t.ready = t.start = nullptr;
 }
 
 // Executes one request on the worker thread. Returns SH_OK or an error status
@@ -126,9 +137,49 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   void* h2d_dst = t.plan ? t.staging : t.dst;
   e = hipStreamWaitEvent(L->copy_stream, t.ready, 0);
   if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(ready)");
+  if (t.start != nullptr) {
+    e = hipEventRecord(t.start, L->copy_stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord(start)");
+  }
+  if (t.image != nullptr) {
+    // Pinned source image: refresh the given pieces, then one DMA straight from it.
+    if (!t.pieces.empty()) {
+      auto f = L->image_fence.find(t.image);
+      if (f != L->image_fence.end()) {
+        e = hipEventSynchronize(f->second);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize(image fence)");
+      }
+      std::vector<sh_copy_item> items(t.pieces.size());
+      for (size_t i = 0; i < t.pieces.size(); ++i) {
+        items[i].dst = (uint8_t*)t.image + (uintptr_t)t.pieces[i].dst;
+        items[i].src = t.pieces[i].src;
+        items[i].bytes = t.pieces[i].bytes;
+      }
+      int st = sh_host_copy_batch(items.data(), items.size(), t.copy_threads);
+      if (st != SH_OK) {
+        err = sh_last_error();
+        return st;
+      }
+    }
+    if (t.src_bytes > 0) {
+      e = hipMemcpyAsync(h2d_dst, t.image, t.src_bytes, hipMemcpyHostToDevice, L->copy_stream);
+      if (e != hipSuccess) return hip_fail(e, "image H2D copy");
+    }
+    hipEvent_t fence = nullptr;
+    auto f = L->image_fence.find(t.image);
+    if (f != L->image_fence.end()) {
+      fence = f->second;
+    } else {
+      e = hipEventCreateWithFlags(&fence, hipEventDisableTiming);
+      if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags(image fence)");
+      L->image_fence[t.image] = fence;
+    }
+    e = hipEventRecord(fence, L->copy_stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord(image fence)");
+  }
   std::vector<sh_copy_item> items;
   items.reserve(t.pieces.size());
-  for (uint64_t c0 = 0; c0 < t.src_bytes; c0 += L->slab_bytes) {
+  for (uint64_t c0 = 0; t.image == nullptr && c0 < t.src_bytes; c0 += L->slab_bytes) {
     const uint64_t c1 = std::min<uint64_t>(t.src_bytes, c0 + L->slab_bytes);
     uint32_t slab = 0;
     double waited = 0;
@@ -273,6 +324,8 @@ extern "C" int sh_loader_destroy(sh_loader* L) {
   (void)hipStreamSynchronize(L->unpack_stream);
   for (auto& kv : L->tickets) give_events(L, kv.second);
   for (hipEvent_t ev : L->spare_events) (void)hipEventDestroy(ev);
+  for (hipEvent_t ev : L->spare_timing_events) (void)hipEventDestroy(ev);
+  for (auto& kv : L->image_fence) (void)hipEventDestroy(kv.second);
   (void)hipStreamDestroy(L->copy_stream);
   (void)hipStreamDestroy(L->unpack_stream);
   delete L;
@@ -328,8 +381,9 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   const uint64_t id = L->next_ticket++;
   Ticket& t = L->tickets[id];
   hipError_t e = take_event(L, &t.ready);
-  if (e == hipSuccess) e = take_event(L, &t.copied);
-  if (e == hipSuccess) e = take_event(L, &t.done);
+  if (e == hipSuccess) e = take_event(L, &t.copied, L->timing);
+  if (e == hipSuccess) e = take_event(L, &t.done, L->timing);
+  if (e == hipSuccess && L->timing) e = take_event(L, &t.start, true);
   if (e == hipSuccess) e = hipEventRecord(t.ready, (hipStream_t)wait_stream);
   if (e != hipSuccess) {
     give_events(L, t);
@@ -347,6 +401,7 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   t.zp_off = req->zp_off;
   t.n_scale = req->n_scale;
   t.copy_threads = req->copy_threads > 0 ? req->copy_threads : L->copy_threads;
+  t.image = req->image;
   L->queue.push_back(id);
   *ticket = id;
   L->cv.notify_one();
@@ -413,5 +468,34 @@ extern "C" int sh_loader_release(sh_loader* L, uint64_t ticket) {
     L->tickets.erase(it);
   }
   if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "sh_loader_release: HIP error %d", (int)e);
+  return SH_OK;
+}
+
+extern "C" int sh_loader_set_timing(sh_loader* L, int enable) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_set_timing: loader is NULL");
+  std::lock_guard<std::mutex> lk(L->mu);
+  L->timing = enable != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_loader_ticket_times(sh_loader* L, uint64_t ticket, void* ref_event, float* out3) {
+  sh::clear_error();
+  if (L == nullptr || ref_event == nullptr || out3 == nullptr)
+    return sh::fail(SH_ERR_INVALID, "sh_loader_ticket_times: NULL argument");
+  hipEvent_t start = nullptr, copied = nullptr, done = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L->mu);
+    Ticket* t = nullptr;
+    if (int st = wait_issued(L, ticket, lk, &t, "sh_loader_ticket_times")) return st;
+    if (t->start == nullptr) return sh::fail(SH_ERR_STATE, "sh_loader_ticket_times: ticket was submitted without timing");
+    start = t->start;
+    copied = t->copied;
+    done = t->done;
+  }
+  SH_HIP(hipEventSynchronize(done));
+  SH_HIP(hipEventElapsedTime(&out3[0], (hipEvent_t)ref_event, start));
+  SH_HIP(hipEventElapsedTime(&out3[1], (hipEvent_t)ref_event, copied));
+  SH_HIP(hipEventElapsedTime(&out3[2], (hipEvent_t)ref_event, done));
   return SH_OK;
 }

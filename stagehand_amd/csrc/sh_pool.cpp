@@ -247,9 +247,12 @@ namespace {
 
 class CopyPool {
  public:
+  // Created on first use and intentionally never destroyed: joining worker
+  // threads from a static destructor at process exit races with the HIP
+  // runtime's and other libraries' own teardown.
   static CopyPool& get() {
-    static CopyPool inst;
-    return inst;
+    static CopyPool* inst = new CopyPool();
+    return *inst;
   }
 
   // Runs fn(i) for i in [0, n) on up to `threads` workers (caller included).
@@ -284,16 +287,10 @@ class CopyPool {
   CopyPool() {
     unsigned hw = std::thread::hardware_concurrency();
     unsigned n = std::max(1u, std::min(hw ? hw : 4u, 16u)) - 1;
-    for (unsigned i = 0; i < n; ++i) workers_.emplace_back([this, i] { loop(i); });
-  }
-  ~CopyPool() {
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      stop_ = true;
-      ++generation_;
+    for (unsigned i = 0; i < n; ++i) {
+      workers_.emplace_back([this, i] { loop(i); });
+      workers_.back().detach();
     }
-    cv_.notify_all();
-    for (auto& t : workers_) t.join();
   }
   void loop(unsigned index) {
     uint64_t seen = 0;

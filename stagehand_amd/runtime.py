@@ -73,7 +73,8 @@ class StagehandRuntime:
                                         nan_inf_check=config.nan_inf_check)
         self._telemetry = StagehandTelemetry(enabled=config.telemetry_enabled, interval_steps=config.telemetry_interval_steps,
                                              output_file=config.telemetry_file if config.telemetry_enabled else None)
-        self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=config.max_inflight_transfers)
+        self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=config.max_inflight_transfers,
+                                           pin_sources=config.pinned_source_cache)
         self._scheduler = StagehandScheduler(
             registry=self._registry, residency=self._residency, transfer_engine=self._engine, budget=self._budget,
             policy=StaticLookaheadPolicy(prefetch_window=config.prefetch_window_blocks,

@@ -185,6 +185,9 @@ class StagehandScheduler:
         self._squareq_layers: dict[str, dict[str, Any]] = {}
         self._module_param_caches: dict[str, dict[str, torch.Tensor]] = {}
         self._plans = PlanCache()
+        # block → event of the asynchronous D2H that moved its module parameters
+        # to host memory at eviction; waited for before those tensors are read
+        self._d2h_fences: dict[str, Any] = {}
 
     # ── step lifecycle ───────────────────────────────────────────────
 
@@ -201,6 +204,7 @@ class StagehandScheduler:
 
     def end_step(self) -> None:
         self._backward_phase = False
+        self._sync_d2h_fences()
         self._engine.reap()
         self._reconcile_file_backed_grads()
         self._telemetry.end_step()
@@ -213,6 +217,46 @@ class StagehandScheduler:
 
     def set_defer_backward_eviction(self, enabled: bool) -> None:
         self._defer_backward_eviction = enabled
+
+    def _sync_d2h_fences(self, block_id: str | None = None) -> None:
+        """Host values of evicted module parameters are final once their D2H event completes."""
+        ids = list(self._d2h_fences) if block_id is None else ([block_id] if block_id in self._d2h_fences else [])
+        for bid in ids:
+            ev = self._d2h_fences.pop(bid)
+            if ev is not None:
+                ev.synchronize()
+
+    def _save_params_to_host(self, block_id: str, module: nn.Module, names: list[str], with_grads: bool = False) -> None:
+        """``param.data = param.data.to("cpu").clone()`` for ``names`` (and grads), without a host sync.
+
+        The reference does this synchronously at eviction (src/stagehand/scheduler.py:1216-1231,
+        :1348-1366), which stalls the host on the whole device queue once per block. Here the
+        copies run on the copy stream into pinned host tensors; the block's fence is waited
+        for before the tensors are read again (next staging, end of step, shutdown).
+        """
+        srcs, targets = [], []
+        for name in names:
+            data = _get_param_data(module, name)
+            if data.device.type != "cpu":
+                srcs.append(data)
+                targets.append(("data", name))
+        if with_grads:
+            for name, param in module.named_parameters():
+                if param.grad is not None and param.grad.device.type != "cpu":
+                    srcs.append(param.grad)
+                    targets.append(("grad", name))
+        if not srcs:
+            return
+        outs, ev = self._engine.d2h_async(srcs)
+        params = dict(module.named_parameters())
+        for (what, name), out in zip(targets, outs):
+            if what == "data":
+                _set_param_data(module, name, out)
+            else:
+                params[name].grad = out
+        if ev is not None:
+            prev = self._d2h_fences.get(block_id)
+            self._d2h_fences[block_id] = ev if prev is None else ev  # later event covers earlier copies on the stream
 
     def _reconcile_file_backed_grads(self) -> None:
         for entry in self._ordered_blocks:
@@ -281,6 +325,7 @@ class StagehandScheduler:
         return layers
 
     def close(self) -> None:
+        self._sync_d2h_fences()
         self._file_tensor_views.clear()
         for fh, mm, view in self._file_maps.values():
             for fn in (view.release, mm.close, fh.close):
@@ -307,6 +352,7 @@ class StagehandScheduler:
     # ── per-block hooks ──────────────────────────────────────────────
 
     def before_block(self, block_id: str) -> None:
+        self._engine._reap_d2h()  # release device buffers whose save-back copies finished
         state = self._residency.get_state(block_id)
         if state == BlockState.GPU_READY:
             self._telemetry.record_prefetch_hit()
@@ -333,6 +379,7 @@ class StagehandScheduler:
 
         self._residency.increment_ref(block_id)
         self._residency.get_entry(block_id).last_used_step = self._current_step
+        self._engine.mark_compute(block_id, start=True)
         self._cursor += 1
         if self._budget.above_high_watermark():
             self._run_eviction(ignore_cooldown=True)
@@ -341,6 +388,7 @@ class StagehandScheduler:
             self._run_eviction(ignore_cooldown=True)
 
     def after_block(self, block_id: str, output: torch.Tensor | None = None) -> None:
+        self._engine.mark_compute(block_id, start=False)
         self._residency.decrement_ref(block_id)
         self._residency.get_entry(block_id).last_used_step = self._current_step
         if self._guards is not None and output is not None and self._config.nan_inf_check:
@@ -425,6 +473,7 @@ class StagehandScheduler:
         """UNLOADED → HOST_STAGED. On a GPU: returns the block's BlockSource (the
         loader fills a pinned slab from it). Without one: a filled pool slab,
         as in src/stagehand/scheduler.py:953-1031."""
+        self._sync_d2h_fences(block_entry.block_id)
         module = block_entry.module_ref()
         if module is None:
             res_entry.param_layout = None
@@ -468,8 +517,10 @@ class StagehandScheduler:
         params = dict(module.named_parameters())
         b = SourceBuilder(block_entry.dtype, block_entry.size_bytes)
         for name, _shape, _dtype, offset, _numel in layout:
-            b.add_param(offset, params[name].data)
-        return self._finish_source(block_entry.block_id, b)
+            b.add_param(offset, params[name].data, mutable=True)
+        source = self._finish_source(block_entry.block_id, b)
+        source.key = None  # every byte is a live module parameter: nothing to keep pinned
+        return source
 
     def _build_source(self, block_entry: BlockEntry, module: nn.Module, layout: Layout):
         if not self._has_cuda:
@@ -512,7 +563,7 @@ class StagehandScheduler:
                 b.add_param(offset, self._get_file_tensor_view(path, spec, view))
                 continue
             if name in mutable and name in params and params[name].data.numel() == numel:
-                b.add_param(offset, params[name].data)
+                b.add_param(offset, params[name].data, mutable=True)
                 continue
             b.add_zero(offset, numel * dtype.itemsize)
 
@@ -577,7 +628,7 @@ class StagehandScheduler:
             if name in mutable and name in params:
                 value = self._module_value(block_entry.block_id, params, name, numel, cache)
                 if value is not None:
-                    b.add_param(offset, value)
+                    b.add_param(offset, value, mutable=True)
                     continue
             b.add_zero(offset, nbytes)
 
@@ -594,6 +645,7 @@ class StagehandScheduler:
         module = block_entry.module_ref()
         if module is None:
             return
+        self._sync_d2h_fences(block_id)
         layout = _build_param_layout(module, block_entry.dtype)
         res_entry.param_layout = layout
         numel = block_entry.size_bytes // block_entry.dtype.itemsize
@@ -686,11 +738,8 @@ class StagehandScheduler:
                 self._residency.transition(block_id, BlockState.EVICTING)
                 self._await_pending_load(block_id)
                 if module is not None:
-                    for param in module.parameters():
-                        if param.data.device.type != "cpu":
-                            param.data = param.data.to("cpu").clone()
-                        if param.grad is not None and param.grad.device.type != "cpu":
-                            param.grad = param.grad.to("cpu")
+                    self._save_params_to_host(block_id, module, [n for n, _ in module.named_parameters()],
+                                              with_grads=True)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -702,10 +751,13 @@ class StagehandScheduler:
                 keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
                 specs = {s.param_name: s for s in block_entry.file_param_specs}
                 if module is not None and res_entry.param_layout is not None:
+                    to_host = []
                     for name, _shape, dtype, _off, _numel in res_entry.param_layout:
                         if name in mutable:
-                            live = _get_param_data(module, name)
-                            _set_param_data(module, name, live.to(live.device if keep_on_gpu else "cpu").clone())
+                            if keep_on_gpu:
+                                _set_param_data(module, name, _get_param_data(module, name).clone())
+                            else:
+                                to_host.append(name)
                         else:
                             restored = False
                             if self._backward_phase and self._defer_backward_eviction:
@@ -714,6 +766,7 @@ class StagehandScheduler:
                                     restored = self._restore_file_param_to_cpu_view(module, name, spec, dtype, block_entry)
                             if not restored:
                                 _set_param_data(module, name, torch.empty(0, dtype=dtype))
+                    self._save_params_to_host(block_id, module, to_host)
                     for name, param in module.named_parameters():
                         if name in mutable and param.grad is not None and param.grad.device.type != "cpu":
                             param.grad = param.grad.to("cpu", non_blocking=True)
@@ -749,17 +802,20 @@ class StagehandScheduler:
         if module is not None and res_entry.param_layout is not None:
             if module_backed:
                 self._await_pending_load(block_id)
-                for name, *_rest in res_entry.param_layout:
-                    _set_param_data(module, name, _get_param_data(module, name).to("cpu").clone())
+                self._save_params_to_host(block_id, module, [n for n, *_ in res_entry.param_layout])
             elif block_entry.file_backed:  # SquareQ-backed blocks are file-backed too (registry BlockEntry.file_backed)
                 resident = set(block_entry.module_param_names)
                 keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
+                to_host = []
                 for name, _shape, dtype, _off, _numel in res_entry.param_layout:
                     if name in resident:
-                        data = _get_param_data(module, name)
-                        _set_param_data(module, name, data.to(data.device if keep_on_gpu else "cpu").clone())
+                        if keep_on_gpu:
+                            _set_param_data(module, name, _get_param_data(module, name).clone())
+                        else:
+                            to_host.append(name)
                     else:
                         _set_param_data(module, name, torch.empty(0, dtype=dtype))
+                self._save_params_to_host(block_id, module, to_host)
             else:
                 _detach_params(module, res_entry.param_layout)
         self._release_device_buffer(res_entry)

@@ -76,6 +76,7 @@ class SourceBuilder:
     _regions: list[tuple] = field(default_factory=list)  # (kind, dst_off, host tensor|None, rows, cols, ld, scale rows)
     _scales: list[torch.Tensor] = field(default_factory=list)
     _zps: list[torch.Tensor | None] = field(default_factory=list)
+    _mutable: list[bool] = field(default_factory=list)  # per region: bytes may change between loads
 
     def __post_init__(self) -> None:
         if self.runtime_dtype not in SUPPORTED_RUNTIME_DTYPES:
@@ -83,10 +84,12 @@ class SourceBuilder:
 
     # ── regions ──────────────────────────────────────────────────────
 
-    def add_param(self, dst_off: int, value: torch.Tensor) -> None:
-        """``dst ← value.to(runtime_dtype)`` (rounded on the device when narrowing)."""
+    def add_param(self, dst_off: int, value: torch.Tensor, mutable: bool = False) -> None:
+        """``dst ← value.to(runtime_dtype)`` (rounded on the device when narrowing).
+        ``mutable`` marks module parameters, whose bytes may change between loads."""
         v = _host_contig(value).reshape(-1)
         rt = self.runtime_dtype
+        self._mutable.append(mutable)
         if v.dtype == rt:
             self._regions.append((KIND_COPY_BYTES, dst_off, v.view(torch.uint8), 1, v.numel() * v.element_size(), 0, 0))
             return
@@ -99,11 +102,13 @@ class SourceBuilder:
         elif rt == torch.float32 and v.dtype == torch.float32:
             self._regions.append((KIND_COPY_BYTES, dst_off, v.view(torch.uint8), 1, v.numel() * 4, 0, 0))
         else:
+            self._mutable.pop()
             raise ValueError(f"no device conversion from {v.dtype} to {rt}")
 
     def add_zero(self, dst_off: int, nbytes: int) -> None:
         if nbytes > 0:
             self._regions.append((KIND_ZERO_BYTES, dst_off, None, 1, nbytes, 0, 0))
+            self._mutable.append(False)
 
     def add_dequant(self, dst_off: int, q_rows: torch.Tensor, in_flat: int, scale: torch.Tensor,
                     zero_point: torch.Tensor | None) -> None:
@@ -120,6 +125,7 @@ class SourceBuilder:
         self._regions.append((kind, dst_off, q.view(torch.uint8).reshape(-1), out_dim, in_flat, ld, out_dim))
         self._scales.append(s)
         self._zps.append(z)
+        self._mutable.append(False)
 
     # ── layout ───────────────────────────────────────────────────────
 
@@ -127,19 +133,26 @@ class SourceBuilder:
         """Returns the block source and, when a kernel is needed, its descriptor table."""
         if all(r[0] in (KIND_COPY_BYTES, KIND_ZERO_BYTES) for r in self._regions):
             pieces = []
-            for kind, dst_off, t, _r, nbytes, _ld, _s in self._regions:
+            mutable = set()
+            for (kind, dst_off, t, _r, nbytes, _ld, _s), mut in zip(self._regions, self._mutable):
+                if mut:
+                    mutable.add(len(pieces))
                 pieces.append((dst_off, t if kind == KIND_COPY_BYTES else _zeros(nbytes)))
-            return BlockSource(pieces=pieces, src_bytes=self.dst_bytes), None
+            key = repr([(o, t.numel()) for o, t in pieces]).encode() + b"|direct|" + str(self.dst_bytes).encode()
+            return BlockSource(pieces=pieces, src_bytes=self.dst_bytes, key=key, mutable=frozenset(mutable)), None
 
         pieces: list[tuple[int, torch.Tensor]] = []
+        mutable = set()
         rows: list[tuple] = []
         cursor = 0
         scale_row = 0
-        for kind, dst_off, t, r, c, ld, srows in self._regions:
+        for (kind, dst_off, t, r, c, ld, srows), mut in zip(self._regions, self._mutable):
             if kind == KIND_ZERO_BYTES:
                 rows.append((kind, 0, dst_off, r, c, 0, 0))
                 continue
             off = _align(cursor)
+            if mut:
+                mutable.add(len(pieces))
             pieces.append((off, t))
             cursor = off + t.numel()
             rows.append((kind, off, dst_off, r, c, ld, scale_row))
@@ -155,9 +168,11 @@ class SourceBuilder:
                 zps = torch.cat([z if z is not None else torch.zeros_like(s) for z, s in zip(self._zps, self._scales)])
                 pieces.append((zp_off, zps.view(torch.uint8)))
                 cursor = zp_off + zps.numel() * 4
+        descs = make_descs(rows)
+        key = descs.tobytes() + f"|{scale_off}|{zp_off}|{cursor}".encode()
         src = BlockSource(pieces=pieces, src_bytes=max(cursor, 1), scale_off=scale_off, zp_off=zp_off,
-                          n_scale=scale_row)
-        return src, make_descs(rows)
+                          n_scale=scale_row, key=key, mutable=frozenset(mutable))
+        return src, descs
 
 
 class PlanCache:

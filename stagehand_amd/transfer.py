@@ -49,10 +49,15 @@ _STALL_LOGS_ENABLED = str(os.getenv("SERENITY_STAGEHAND_STALL_LOGS", "0")).strip
 class NativeEvent:
     """A native HIP event with the ``query``/``synchronize`` face of ``torch.cuda.Event``."""
 
-    def __init__(self) -> None:
+    def __init__(self, timing: bool = False) -> None:
         h = ctypes.c_void_p()
-        _native.call("sh_event_create", 0, ctypes.byref(h))
+        _native.call("sh_event_create", int(timing), ctypes.byref(h))
         self.handle = h
+
+    def elapsed_ms(self, later: "NativeEvent") -> float:
+        ms = ctypes.c_float()
+        _native.call("sh_event_elapsed_ms", self.handle, later.handle, ctypes.byref(ms))
+        return ms.value
 
     def record(self, stream_handle: int) -> None:
         _native.call("sh_event_record", self.handle, stream_handle)
@@ -99,6 +104,10 @@ class BlockSource:
     scale_off: int = -1
     zp_off: int = -1
     n_scale: int = 0
+    # pinned-image caching: a layout signature, and the pieces whose bytes may
+    # change between loads (module parameters); None key = not cacheable
+    key: bytes | None = None
+    mutable: frozenset = frozenset()
 
 
 def _current_stream_handle() -> int:
@@ -114,8 +123,14 @@ class AsyncTransferEngine:
         max_inflight: int = 2,
         copy_stream: torch.cuda.Stream | None = None,
         copy_threads: int | None = None,
+        pin_sources: bool = False,
     ) -> None:
         self._pool = pool
+        # pin_sources: keep one pinned host image per cacheable block source and
+        # DMA straight from it (no staging copy after the first load)
+        self._pin_sources = pin_sources
+        self._images: dict[str, tuple[bytes, int, int]] = {}  # block → (key, pinned ptr, bytes)
+        self.pinned_image_bytes = 0
         self._max_inflight = max_inflight
         self._has_cuda = torch.cuda.is_available()
         self._lock = threading.Lock()
@@ -126,6 +141,16 @@ class AsyncTransferEngine:
         self._owned_stream = None
         self._copy_stream = None
         self._copy_threads = copy_threads or min(16, os.cpu_count() or 1)
+        # bytes actually sent host→device / device→host (a SquareQ block sends its
+        # int8 source, not its bf16 size; telemetry keeps the reference's block sizes)
+        self.bytes_h2d = 0
+        self.bytes_d2h = 0
+        self.loads = 0
+        self._pending_d2h: list[tuple[NativeEvent, list]] = []
+        # optional device timeline (start_trace / stop_trace)
+        self._trace_ref: NativeEvent | None = None
+        self._trace_loads: list[tuple[str, int, float, float, float]] = []
+        self._trace_compute: list[tuple[str, NativeEvent, NativeEvent]] = []
         if self._has_cuda:
             _native.call("sh_set_device", torch.cuda.current_device())
             if copy_stream is not None:
@@ -176,6 +201,7 @@ class AsyncTransferEngine:
             handle.event = NativeEvent()
             handle.event.record(cs)
             handle.keepalive = [gpu_dest]
+            self.bytes_h2d += size
         else:
             gpu_dest.view(-1).view(torch.uint8).copy_(host_slab.buffer[:size])
             handle.completed = True
@@ -197,6 +223,7 @@ class AsyncTransferEngine:
             handle.event = NativeEvent()
             handle.event.record(cs)
             handle.keepalive = [gpu_src]
+            self.bytes_d2h += size
         else:
             host_slab.buffer[:size].copy_(gpu_src.reshape(-1).view(torch.uint8))
             handle.completed = True
@@ -213,9 +240,15 @@ class AsyncTransferEngine:
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
         self._wait_for_slot()
         handle = self._make_handle(block_id, "load", source.src_bytes)
-        items = np.zeros(len(source.pieces), dtype=COPY_ITEM_DTYPE)
+        image = 0
+        pieces = source.pieces
+        if self._pin_sources and source.key is not None and source.src_bytes > 0:
+            image, fresh = self._image_for(block_id, source)
+            if not fresh:
+                pieces = [p for i, p in enumerate(source.pieces) if i in source.mutable]
+        items = np.zeros(len(pieces), dtype=COPY_ITEM_DTYPE)
         keep: list = [gpu_dest]
-        for i, (off, t) in enumerate(source.pieces):
+        for i, (off, t) in enumerate(pieces):
             if t.device.type != "cpu" or not t.is_contiguous():
                 raise ValueError(f"block {block_id}: piece {i} must be a contiguous host tensor")
             items[i] = (off, t.data_ptr(), t.numel() * t.element_size())
@@ -231,6 +264,7 @@ class AsyncTransferEngine:
         req[0]["zp_off"] = source.zp_off
         req[0]["n_scale"] = source.n_scale
         req[0]["copy_threads"] = self._copy_threads
+        req[0]["image"] = image
         if source.plan is not None:
             staging = torch.empty(max(source.src_bytes, 1), dtype=torch.uint8, device=gpu_dest.device)
             keep.append(staging)
@@ -245,9 +279,144 @@ class AsyncTransferEngine:
             self._raise_transfer(st, block_id, "load")
         handle.ticket = ticket.value
         handle.keepalive = keep
+        self.bytes_h2d += source.src_bytes
+        self.loads += 1
         with self._lock:
             self._inflight.append(handle)
         return handle
+
+    def _image_for(self, block_id: str, source: BlockSource) -> tuple[int, bool]:
+        """Pinned image for ``block_id``; fresh=True when it must be filled with every piece."""
+        hit = self._images.get(block_id)
+        if hit is not None and hit[0] == source.key and hit[2] >= source.src_bytes:
+            return hit[1], False
+        if hit is not None:
+            # the loader fences re-use of an image, not its release: drain before freeing
+            self.drain()
+            _native.call("sh_host_free", hit[1])
+            self.pinned_image_bytes -= hit[2]
+            del self._images[block_id]
+        ptr = ctypes.c_void_p()
+        _native.call("sh_host_alloc", source.src_bytes, ctypes.byref(ptr))
+        self._images[block_id] = (source.key, ptr.value, source.src_bytes)
+        self.pinned_image_bytes += source.src_bytes
+        return ptr.value, True
+
+    def free_images(self) -> None:
+        if not self._images:
+            return
+        self.drain()
+        if self._loader is not None:
+            # every copy out of the images has completed once the loader's streams drain
+            cs, us = self.loader_streams()
+            _native.call("sh_stream_sync", cs)
+            _native.call("sh_stream_sync", us)
+        for _key, ptr, nbytes in self._images.values():
+            _native.call("sh_host_free", ptr)
+            self.pinned_image_bytes -= nbytes
+        self._images.clear()
+
+    # ── device timeline ──────────────────────────────────────────────
+
+    def start_trace(self) -> None:
+        """Time every later block load (copy start / copy end / done) and the compute
+        spans the scheduler marks, relative to an event recorded now."""
+        if not self._has_cuda:
+            return
+        _native.call("sh_loader_set_timing", self._loader_handle(), 1)
+        self._trace_ref = NativeEvent(timing=True)
+        self._trace_ref.record(_current_stream_handle())
+        self._trace_loads = []
+        self._trace_compute = []
+
+    @property
+    def tracing(self) -> bool:
+        return self._trace_ref is not None
+
+    def mark_compute(self, block_id: str, start: bool) -> None:
+        if self._trace_ref is None:
+            return
+        ev = NativeEvent(timing=True)
+        ev.record(_current_stream_handle())
+        if start:
+            self._trace_compute.append((block_id, ev, ev))
+        else:
+            for i in range(len(self._trace_compute) - 1, -1, -1):
+                bid, s_ev, e_ev = self._trace_compute[i]
+                if bid == block_id and e_ev is s_ev:
+                    self._trace_compute[i] = (bid, s_ev, ev)
+                    break
+
+    def stop_trace(self) -> dict:
+        """Drains and returns {"loads": [(block, bytes, start, copied, done) ms], "compute": [(block, start, end) ms]}."""
+        if self._trace_ref is None:
+            return {"loads": [], "compute": []}
+        self.drain()
+        torch.cuda.synchronize()
+        ref = self._trace_ref
+        compute = [(bid, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev)) for bid, s_ev, e_ev in self._trace_compute]
+        out = {"loads": list(self._trace_loads), "compute": compute}
+        _native.call("sh_loader_set_timing", self._loader_handle(), 0)
+        self._trace_ref = None
+        self._trace_loads, self._trace_compute = [], []
+        return out
+
+    def _record_ticket_times(self, handle: TransferHandle) -> None:
+        if self._trace_ref is None or handle.ticket is None:
+            return
+        out = (ctypes.c_float * 3)()
+        st = _native.lib().sh_loader_ticket_times(self._loader, handle.ticket, self._trace_ref.handle, out)
+        if st == _native.SH_OK:
+            self._trace_loads.append((handle.block_id, handle.size_bytes, out[0], out[1], out[2]))
+
+    # ── asynchronous parameter save-back ─────────────────────────────
+
+    def d2h_async(self, tensors: list[torch.Tensor]) -> tuple[list[torch.Tensor], NativeEvent | None]:
+        """Copies device tensors into new pinned host tensors on the copy stream.
+
+        Returns the host tensors and the event that marks their completion (None
+        without a GPU, where the copies are synchronous). The device tensors are
+        kept alive until the copies complete (``reap``/``drain``), so the caller
+        may drop its references at once. Ordering: the copies start after the
+        work queued so far on the current stream.
+        """
+        if not self._has_cuda:
+            return [t.detach().to("cpu").clone() for t in tensors], None
+        cs = self._copy_stream.cuda_stream
+        self._fence_copy_stream(cs)
+        outs, keep = [], []
+        for t in tensors:
+            src = t.detach()
+            if src.device.type == "cpu":
+                outs.append(src.clone())
+                continue
+            src = src.contiguous()
+            out = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+            nbytes = src.numel() * src.element_size()
+            self._check_copy(_native.lib().sh_memcpy_d2h_async(out.data_ptr(), src.data_ptr(), nbytes, cs), "params", "d2h")
+            self.bytes_d2h += nbytes
+            outs.append(out)
+            keep.append(src)
+        ev = NativeEvent()
+        ev.record(cs)
+        with self._lock:
+            self._pending_d2h.append((ev, keep))
+        return outs, ev
+
+    def _reap_d2h(self, block: bool = False) -> None:
+        """Drops the device references of completed save-back copies (they complete in order)."""
+        while True:
+            with self._lock:
+                if not self._pending_d2h:
+                    return
+                ev, _keep = self._pending_d2h[0]
+            if block:
+                ev.synchronize()
+            elif not ev.query():
+                return
+            with self._lock:
+                if self._pending_d2h and self._pending_d2h[0][0] is ev:
+                    self._pending_d2h.pop(0)
 
     # ── completion ───────────────────────────────────────────────────
 
@@ -312,6 +481,7 @@ class AsyncTransferEngine:
             return len(self._inflight)
 
     def reap(self) -> int:
+        self._reap_d2h()
         with self._lock:
             before = len(self._inflight)
             self._reap_completed_locked()
@@ -325,10 +495,12 @@ class AsyncTransferEngine:
                 break
             for h in remaining:
                 self.wait(h)
+        self._reap_d2h(block=True)
 
     def shutdown(self) -> None:
         try:
             self.drain()
+            self.free_images()
         finally:
             if self._loader is not None:
                 _native.call("sh_loader_destroy", self._loader)
@@ -371,23 +543,40 @@ class AsyncTransferEngine:
         return TransferHandle(hid, block_id, direction, None, time.monotonic(), size_bytes)
 
     def _wait_for_slot(self) -> None:
+        """Backpressure: block while ``max_inflight`` transfers are outstanding.
+
+        The reference polls in 1 ms condition waits (src/stagehand/transfer.py:258-276);
+        here the host sleeps in a native wait on the oldest transfer (copies on one
+        stream complete in order), so a freed slot is seen at once. A wait above
+        1 ms is logged at debug level: in a PCIe-bound stream it is the normal pacing.
+        """
+        self._reap_d2h()
         t0 = time.monotonic()
-        warned = False
-        with self._cond:
-            while len(self._inflight) >= self._max_inflight:
+        while True:
+            with self._cond:
                 self._reap_completed_locked()
                 if len(self._inflight) < self._max_inflight:
                     break
-                self._cond.wait(timeout=0.001)
-                if not warned and (time.monotonic() - t0) * 1000.0 > 1.0:
-                    log.warning("AsyncTransferEngine: backpressure wait %.2f ms", (time.monotonic() - t0) * 1000.0)
-                    warned = True
+                oldest = self._inflight[0]
+            if oldest.ticket is not None:
+                st = _native.lib().sh_loader_sync(self._loader, oldest.ticket)
+                if st != _native.SH_OK:
+                    self._raise_transfer(st, oldest.block_id, oldest.direction)
+            elif oldest.event is not None:
+                oldest.event.synchronize()
+            else:
+                with self._cond:
+                    self._cond.wait(timeout=0.001)
+        waited_ms = (time.monotonic() - t0) * 1000.0
+        if waited_ms > 1.0:
+            log.debug("AsyncTransferEngine: backpressure wait %.2f ms", waited_ms)
 
     def _complete_handle(self, handle: TransferHandle) -> None:
         if handle.completed:
             return
         handle.completed = True
         if handle.ticket is not None and self._loader is not None:
+            self._record_ticket_times(handle)
             _native.call("sh_loader_release", self._loader, handle.ticket)
             handle.ticket = None
         handle.keepalive = []
@@ -414,6 +603,7 @@ class AsyncTransferEngine:
         for h in done:
             h.completed = True
             if h.ticket is not None and self._loader is not None:
+                self._record_ticket_times(h)
                 _native.lib().sh_loader_release(self._loader, h.ticket)
                 h.ticket = None
             h.keepalive = []

@@ -70,3 +70,140 @@ def config2_device_inputs(regions: list[Region], variant: str, seed: int, device
         src = torch.randn(n, device=device, generator=gen, dtype=torch.float32) * 0.02
         return src, None
     raise ValueError(variant)
+
+
+# ── Flux-style DiT (configs 3-5) ─────────────────────────────────────────────
+
+import math as _math
+
+from torch import nn as _nn
+from torch.nn import functional as _F
+
+
+class _QKNorm(_nn.Module):
+    def __init__(self, head_dim: int) -> None:
+        super().__init__()
+        self.query_norm = _nn.RMSNorm(head_dim, eps=1e-6)
+        self.key_norm = _nn.RMSNorm(head_dim, eps=1e-6)
+
+
+def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """(B, H, S, D) scaled dot-product attention on the fused (flash) kernel only."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        return _F.scaled_dot_product_attention(q.contiguous(), k.contiguous(), v.contiguous())
+
+
+def _split_heads(x: torch.Tensor, heads: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    b, s, three_h = x.shape
+    d = three_h // (3 * heads)
+    qkv = x.view(b, s, 3, heads, d).permute(2, 0, 3, 1, 4)
+    return qkv[0], qkv[1], qkv[2]
+
+
+class DoubleStreamBlock(_nn.Module):
+    """Image and text streams with joint attention (Flux double-stream layout)."""
+
+    def __init__(self, hidden: int, heads: int, mlp_ratio: float) -> None:
+        super().__init__()
+        mlp = int(hidden * mlp_ratio)
+        self.heads = heads
+        for side in ("img", "txt"):
+            setattr(self, f"{side}_mod", _nn.Linear(hidden, 6 * hidden))
+            setattr(self, f"{side}_qkv", _nn.Linear(hidden, 3 * hidden))
+            setattr(self, f"{side}_qk_norm", _QKNorm(hidden // heads))
+            setattr(self, f"{side}_proj", _nn.Linear(hidden, hidden))
+            setattr(self, f"{side}_mlp", _nn.Sequential(_nn.Linear(hidden, mlp), _nn.GELU(approximate="tanh"),
+                                                         _nn.Linear(mlp, hidden)))
+
+    def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        h = img.shape[-1]
+        sv = _F.silu(vec)[:, None, :]
+        im = self.img_mod(sv).chunk(6, dim=-1)
+        tm = self.txt_mod(sv).chunk(6, dim=-1)
+        img_n = _F.layer_norm(img, (h,), eps=1e-6) * (1 + im[1]) + im[0]
+        txt_n = _F.layer_norm(txt, (h,), eps=1e-6) * (1 + tm[1]) + tm[0]
+        iq, ik, iv = _split_heads(self.img_qkv(img_n), self.heads)
+        tq, tk, tv = _split_heads(self.txt_qkv(txt_n), self.heads)
+        iq, ik = self.img_qk_norm.query_norm(iq), self.img_qk_norm.key_norm(ik)
+        tq, tk = self.txt_qk_norm.query_norm(tq), self.txt_qk_norm.key_norm(tk)
+        q, k, v = torch.cat([tq, iq], 2), torch.cat([tk, ik], 2), torch.cat([tv, iv], 2)
+        attn = _attention(q, k, v).permute(0, 2, 1, 3).reshape(img.shape[0], -1, h)
+        t_attn, i_attn = attn[:, : txt.shape[1]], attn[:, txt.shape[1]:]
+        img = img + im[2] * self.img_proj(i_attn)
+        img = img + im[5] * self.img_mlp(_F.layer_norm(img, (h,), eps=1e-6) * (1 + im[4]) + im[3])
+        txt = txt + tm[2] * self.txt_proj(t_attn)
+        txt = txt + tm[5] * self.txt_mlp(_F.layer_norm(txt, (h,), eps=1e-6) * (1 + tm[4]) + tm[3])
+        return img, txt
+
+
+class SingleStreamBlock(_nn.Module):
+    """Fused QKV+MLP-in projection and fused output projection (Flux single-stream layout)."""
+
+    def __init__(self, hidden: int, heads: int, mlp_ratio: float) -> None:
+        super().__init__()
+        self.hidden, self.heads, self.mlp = hidden, heads, int(hidden * mlp_ratio)
+        self.linear1 = _nn.Linear(hidden, 3 * hidden + self.mlp)
+        self.linear2 = _nn.Linear(hidden + self.mlp, hidden)
+        self.qk_norm = _QKNorm(hidden // heads)
+        self.modulation = _nn.Linear(hidden, 3 * hidden)
+
+    def forward(self, x: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+        h = self.hidden
+        shift, scale, gate = self.modulation(_F.silu(vec)[:, None, :]).chunk(3, dim=-1)
+        xn = _F.layer_norm(x, (h,), eps=1e-6) * (1 + scale) + shift
+        qkv, mlp_in = torch.split(self.linear1(xn), [3 * h, self.mlp], dim=-1)
+        q, k, v = _split_heads(qkv, self.heads)
+        q, k = self.qk_norm.query_norm(q), self.qk_norm.key_norm(k)
+        attn = _attention(q, k, v).permute(0, 2, 1, 3).reshape(x.shape[0], -1, h)
+        return x + gate * self.linear2(torch.cat([attn, _F.gelu(mlp_in, approximate="tanh")], dim=-1))
+
+
+class FluxStyleDiT(_nn.Module):
+    """19 double-stream + 38 single-stream blocks, hidden 3072, 24 heads, MLP ratio 4 by default
+    (11.84 B block parameters). Only the blocks are built: the benchmark feeds
+    latent / text token activations and a conditioning vector directly."""
+
+    def __init__(self, depth_double: int = 19, depth_single: int = 38, hidden: int = 3072, heads: int = 24,
+                 mlp_ratio: float = 4.0) -> None:
+        super().__init__()
+        self.double_blocks = _nn.ModuleList(DoubleStreamBlock(hidden, heads, mlp_ratio) for _ in range(depth_double))
+        self.single_blocks = _nn.ModuleList(SingleStreamBlock(hidden, heads, mlp_ratio) for _ in range(depth_single))
+
+    def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+        for blk in self.double_blocks:
+            img, txt = blk(img, txt, vec)
+        x = torch.cat([txt, img], dim=1)
+        for blk in self.single_blocks:
+            x = blk(x, vec)
+        return x[:, txt.shape[1]:]
+
+
+DIT_BLOCK_PATTERN = r"^(double_blocks|single_blocks)\.\d+$"
+
+
+def dit_linear_layers(model: _nn.Module) -> list[tuple[str, _nn.Linear]]:
+    return [(n, m) for n, m in model.named_modules() if isinstance(m, _nn.Linear)]
+
+
+def dit_forward_flops(model: FluxStyleDiT, img_tokens: int, txt_tokens: int) -> float:
+    """Matmul FLOPs of one forward (2 per multiply-add; attention score and value products included)."""
+    flops = 0.0
+    for name, lin in dit_linear_layers(model):
+        tokens = img_tokens if ".img_" in name else txt_tokens if ".txt_" in name else img_tokens + txt_tokens
+        if name.endswith("_mod") or name.endswith("modulation"):
+            tokens = 1
+        flops += 2.0 * tokens * lin.in_features * lin.out_features
+    s = img_tokens + txt_tokens
+    for blk in list(model.double_blocks) + list(model.single_blocks):
+        hidden = blk.img_proj.in_features if isinstance(blk, DoubleStreamBlock) else blk.hidden
+        flops += 2 * 2.0 * s * s * hidden
+    return flops
+
+
+def materialize_norms_(model: _nn.Module, device: str = "cpu") -> None:
+    """Gives a meta-device model real RMSNorm weights (ones); everything else stays meta."""
+    for mod in model.modules():
+        if isinstance(mod, _nn.RMSNorm) and mod.weight is not None:
+            mod.weight = _nn.Parameter(torch.ones(mod.weight.shape, device=device), requires_grad=False)

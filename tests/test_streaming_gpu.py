@@ -172,7 +172,9 @@ def test_module_backed_training_round_trip():
     base_mb = torch.cuda.memory_allocated() / 2**20
     cfg = _config(vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb), prefetch_window_blocks=1)
     rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, inference_mode=False)
-    x = torch.randn(4, 64).to(torch.bfloat16).cuda()
+    # activations entering the blocks carry grad (as they do after an embedding),
+    # so each block's full backward hook fires after its own backward ops
+    x = torch.randn(4, 64).to(torch.bfloat16).cuda().requires_grad_()
     rt.begin_step(0)
     with rt.managed_forward(), rt.managed_backward():
         y = model(x)
@@ -186,3 +188,100 @@ def test_module_backed_training_round_trip():
         assert p1.grad is not None, n1
         assert torch.allclose(p1.grad.float().cpu(), p2.grad.float().cpu(), atol=1e-3, rtol=1e-2), n1
     rt.shutdown()
+
+
+def test_dit_squareq_streaming_matches_unstreamed(tmp_path):
+    """A small Flux-style DiT built on the meta device, SquareQ-backed, streamed in block
+    mode, equals the same DiT run unstreamed with the host-dequantised weights."""
+    import sys
+    from pathlib import Path as _P
+
+    sys.path.insert(0, str(_P(__file__).resolve().parent.parent))
+    from bench import write_dit_squareq
+    from stagehand_amd.workloads import DIT_BLOCK_PATTERN, FluxStyleDiT, dit_linear_layers, materialize_norms_
+
+    kw = dict(depth_double=2, depth_single=3, hidden=256, heads=2, mlp_ratio=4.0)
+    with torch.device("meta"):
+        model = FluxStyleDiT(**kw)
+    model.requires_grad_(False)
+    materialize_norms_(model)
+    path = tmp_path / "dit.fpk"
+    layers = write_dit_squareq(model, path, seed=5)
+
+    ref = FluxStyleDiT(**kw)
+    with torch.no_grad():
+        for name, lin in dit_linear_layers(ref):
+            L = layers[name]
+            lin.weight.copy_(expected_squareq_weight(L, lin.out_features, lin.in_features, torch.bfloat16).float())
+            lin.bias.copy_(L["bias"].float())
+        for mod in ref.modules():
+            if isinstance(mod, torch.nn.RMSNorm):
+                mod.weight.fill_(1.0)
+    ref = ref.to(device="cuda", dtype=torch.bfloat16)
+
+    cfg = _config(pinned_pool_mb=16, pinned_slab_mb=1, prefetch_window_blocks=2, max_inflight_transfers=3)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=DIT_BLOCK_PATTERN, dtype=torch.bfloat16, inference_mode=True)
+    assert rt.convert_registry_to_file_backed(str(path)) == 2 * 20 + 3 * 6
+    g = torch.Generator(device="cuda").manual_seed(0)
+    img = torch.randn(1, 64, 256, device="cuda", generator=g).to(torch.bfloat16)
+    txt = torch.randn(1, 16, 256, device="cuda", generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, 256, device="cuda", generator=g).to(torch.bfloat16)
+    outs = []
+    for step in range(2):
+        rt.begin_step(step)
+        with torch.no_grad(), rt.managed_forward():
+            outs.append(model(img, txt, vec))
+        rt.end_step()
+    with torch.no_grad():
+        want = ref(img, txt, vec)
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.equal(_bits(y), _bits(want))
+    # PCIe bytes: int8 weights + fp32 scales + bf16 biases/norms, about half the bf16 block bytes
+    sent = rt.engine.bytes_h2d
+    bf16 = sum(e.size_bytes for e in rt.registry.blocks_in_order())
+    assert sent < 0.6 * 2 * bf16
+    rt.shutdown()
+
+
+def test_pinned_source_images_refresh_mutable_params(tmp_path):
+    """With pinned source images, later loads DMA from the image; module-backed
+    (mutable) parameters are re-gathered, so changes to them are streamed."""
+    model = init_(TinyStack(n=4, hidden=64, mlp=4))
+    payload = squareq_payload(model)
+    path = tmp_path / "tiny.fpk"
+    torch.save(payload, path)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    model = model.to(torch.bfloat16)
+    base_mb = torch.cuda.memory_allocated() / 2**20
+    cfg = _config(vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb), prefetch_window_blocks=1,
+                  pinned_source_cache=True)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, inference_mode=True)
+    rt.convert_registry_to_file_backed(str(path))
+    x = torch.randn(3, 64).to(torch.bfloat16).cuda()
+    y0 = _run_blocks(rt, model, x, steps=2)
+    assert torch.equal(_bits(y0[0]), _bits(y0[1]))
+    assert rt.engine.pinned_image_bytes > 0
+    # change block 0's norm weight (module-backed) while the block is evicted to CPU
+    e0 = rt.residency.get_entry("blocks.0")
+    if e0.gpu_tensor is not None:
+        rt.scheduler._evict_block("blocks.0")
+    with torch.no_grad():
+        model.blocks[0].norm.weight.mul_(2.0)
+    y1 = _run_blocks(rt, model, x, steps=1)[0]
+    assert not torch.equal(_bits(y1), _bits(y0[0]))
+    rt.shutdown()
+    # reference: an identical model with the same change, streamed through the staged (non-pinned) path
+    model2 = init_(TinyStack(n=4, hidden=64, mlp=4))
+    for p in model2.parameters():
+        p.requires_grad_(False)
+    model2 = model2.to(torch.bfloat16)
+    with torch.no_grad():
+        model2.blocks[0].norm.weight.mul_(2.0)
+    rt2 = stagehand.StagehandRuntime(model2, _config(), block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                     inference_mode=True)
+    rt2.convert_registry_to_file_backed(str(path))
+    y2 = _run_blocks(rt2, model2, x, steps=1)[0]
+    assert torch.equal(_bits(y1), _bits(y2))
+    rt2.shutdown()
