@@ -104,6 +104,29 @@ def d2d_copy_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
     return reps * 2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9
 
 
+def copy_kernel_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
+    """Read+write ceiling of a 128-bit stream kernel on this device: a byte copy
+    through the unpack kernel, timed on the stream it is launched on."""
+    import torch
+
+    from stagehand_amd.unpack import KIND_COPY_BYTES, UnpackPlan, make_descs
+
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    plan = UnpackPlan(make_descs([(KIND_COPY_BYTES, 0, 0, 1, nbytes, 0, 0)]))
+    stream = torch.cuda.current_stream()
+    plan.run(a, b, stream=stream)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(reps):
+        plan.run(a, b, stream=stream)
+    e.record(stream)
+    torch.cuda.synchronize()
+    plan.close()
+    return reps * 2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9
+
+
 def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
     """The reference's host dequant (torch CPU ops) on a bounded sample; bit-checked against dst."""
     import torch
@@ -593,6 +616,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("d2d copy and pinned H2D")
         result["d2d_copy_gbps"] = round(d2d_copy_gbps(), 2)
+        result["copy_kernel_gbps"] = round(copy_kernel_gbps(), 2)
         result["pcie"] = {"h2d_pinned_gbps": round(pinned_h2d_gbps(), 2), "transfer_bytes": 1 << 30, "reps": 10}
         args.pcie_peak_gbps = result["pcie"]["h2d_pinned_gbps"]
 
