@@ -406,6 +406,92 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool) -> dict:
     return res
 
 
+def _dit_host_bf16(seed: int):
+    """The 12B DiT with every block parameter in host memory as bf16: N(0, 0.02)
+    drawn on the device (fast), RMSNorm weights ones; frozen."""
+    import torch
+
+    from stagehand_amd.workloads import FluxStyleDiT
+
+    with torch.device("meta"):
+        model = FluxStyleDiT()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for mod in model.modules():
+        for name, prm in list(mod.named_parameters(recurse=False)):
+            if isinstance(mod, torch.nn.RMSNorm):
+                t = torch.ones(prm.shape, dtype=torch.bfloat16)
+            else:
+                t = (torch.randn(prm.shape, device="cuda", generator=g) * 0.02).to(torch.bfloat16).cpu()
+            setattr(mod, name, torch.nn.Parameter(t, requires_grad=False))
+    return model
+
+
+def turbo_leg(args) -> dict:
+    """The config-3 DiT (bf16, 23.7 GB of blocks) through the turbo window engine:
+    every block pinned on the host, a window of 3 device slots, one H2D per block
+    per step. Run twice: the engine's own layout (contiguous slots, no write-back
+    of frozen blocks) and the reference's layout (a slot tensor per parameter,
+    write-back of every evicted block)."""
+    import gc
+
+    import torch
+
+    from stagehand_amd.turbo import TurboConductor
+    from stagehand_amd.workloads import DIT_BLOCK_PATTERN, dit_forward_flops
+
+    img, txt, vec = _dit_inputs(args.seed)
+    out = {"workload": "config3 bf16 Flux-style DiT (19 double + 38 single blocks, 11.84 B params), module-backed "
+                       "weights pinned on the host, turbo window of 3 slots, 4096 image + 512 text tokens, inference"}
+    for label, contiguous, wb in (("engine_layout", True, "auto"), ("reference_layout", False, "always")):
+        t0 = time.perf_counter()
+        model = _dit_host_bf16(args.seed)
+        flops = dit_forward_flops(model, 4096, 512)
+        cond = TurboConductor(model, block_pattern=DIT_BLOCK_PATTERN, dtype=torch.bfloat16,
+                              contiguous_slots=contiguous, writeback=wb)
+        cond.prepare()
+        gc.collect()
+        prep_s = time.perf_counter() - t0
+        handles = cond.install_hooks()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+
+        def step():
+            with torch.no_grad():
+                return model(img, txt, vec)
+
+        for _ in range(args.dit_warmup):
+            step()
+        torch.cuda.synchronize()
+        h0, d0 = cond.engine.bytes_moved()
+        t1 = time.perf_counter()
+        for _ in range(args.dit_steps):
+            y = step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t1
+        h1, d1 = cond.engine.bytes_moved()
+        cond.start_trace()
+        step()
+        timeline = timeline_stats(cond.stop_trace(), getattr(args, "pcie_peak_gbps", None))
+        ms = wall / args.dit_steps * 1e3
+        h2d = (h1 - h0) // args.dit_steps
+        res = {"ms_per_step": round(ms, 2), "h2d_bytes_per_step": h2d, "d2h_bytes_per_step": (d1 - d0) // args.dit_steps,
+               "h2d_gbps": round(h2d / (ms * 1e-3) / 1e9, 2), "forward_tflop": round(flops / 1e12, 2),
+               "peak_vram_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2), "prepare_s": round(prep_s, 1),
+               "out_finite": bool(torch.isfinite(y.float()).all()), "steps": args.dit_steps, "warmup": args.dit_warmup,
+               "timeline": timeline}
+        if getattr(args, "pcie_peak_gbps", None):
+            res["pcie_frac"] = round(res["h2d_gbps"] / args.pcie_peak_gbps, 4)
+        out[label] = res
+        log(f"turbo/{label}: {res}")
+        for h in handles:
+            h.remove()
+        cond.shutdown(restore_params=False)
+        del cond, model, y
+        gc.collect()
+        torch.cuda.empty_cache()
+    return out
+
+
 def dit_leg(kind: str, args) -> dict:
     """Streams the 19+38-block Flux-style DiT through StagehandRuntime block mode.
 
@@ -505,6 +591,7 @@ def main() -> int:
     ap.add_argument("--workdir", default=None, help="directory for the DiT weight files (default: system temp)")
     ap.add_argument("--dit-modes", default="staged", choices=["staged", "pinned", "both"])
     ap.add_argument("--only-dit", action="store_true", help="skip the config-2 kernel legs (profiling the DiT stream)")
+    ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -531,6 +618,8 @@ def main() -> int:
             out["dit_squareq"] = dit_leg("squareq", args)
         if args.dit in ("file", "both"):
             out["dit_file"] = dit_leg("file", args)
+        if args.turbo == "on":
+            out["turbo"] = turbo_leg(args)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -647,6 +736,9 @@ def main() -> int:
         log("dit: config 3 (file-backed bf16) streaming")
         result["dit_file"] = dit_leg("file", args)
         torch.cuda.empty_cache()
+    if args.turbo == "on":
+        log("turbo: config 3 DiT through the window engine")
+        result["turbo"] = turbo_leg(args)
 
     print(json.dumps(result), flush=True)
     return 0

@@ -290,6 +290,57 @@ int sh_loader_release(sh_loader* loader, uint64_t ticket);
 int sh_loader_set_timing(sh_loader* loader, int enable);
 int sh_loader_ticket_times(sh_loader* loader, uint64_t ticket, void* ref_event, float* out3);
 
+/* ───────────────────────── turbo window engine ─────────────────────────
+ * A fixed window of device slots that blocks rotate through: the HIP rewrite
+ * of the reference's Rust TransferEngine (turbo_src/engine.rs:51-422, Python
+ * surface turbo_src/lib.rs:14-126). Every block's parameters live in ONE
+ * pinned host region (params at 256-byte aligned offsets), so a block moves in
+ * one hipMemcpyAsync when its slot is a contiguous device buffer
+ * (sh_turbo_set_slot_buffer). Ordering is device-side only: the compute stream
+ * waits on the block's own H2D event (no host synchronisation, no shared
+ * event), an eviction orders its D2H after the compute queued so far, and a
+ * slot freed by an eviction is reused by a prefetch through a device wait on
+ * the slot's fence. Blocks marked write-back off (frozen weights) skip the
+ * D2H. Device pointers in slots belong to the caller (PyTorch tensors),
+ * pinned host memory to the engine (engine.rs:132-138, 396-422).
+ * Errors: a bad direction is SH_ERR_INVALID (ValueError, lib.rs:59-61); every
+ * other failure, including "No free GPU slots" (engine.rs:189) and an index
+ * out of range, is SH_ERR_STATE or SH_ERR_HIP (RuntimeError, lib.rs:38-40). */
+enum sh_turbo_location { SH_TURBO_CPU = 0, SH_TURBO_GPU = 1, SH_TURBO_H2D = 2, SH_TURBO_D2H = 3 };
+enum sh_turbo_direction { SH_TURBO_FORWARD = 0, SH_TURBO_BACKWARD = 1 };
+typedef struct sh_turbo sh_turbo;
+int sh_turbo_create(sh_turbo** out);                                      /* TransferEngine::new, engine.rs:67-79 */
+int sh_turbo_destroy(sh_turbo* t);                                        /* Drop, engine.rs:396-422 */
+int sh_turbo_register_block(sh_turbo* t, const uint64_t* sizes, uint32_t n, uint32_t* index); /* engine.rs:82-99 */
+int sh_turbo_initialize(sh_turbo* t, int device, uint32_t window);        /* engine.rs:102-156 */
+int sh_turbo_stage_block(sh_turbo* t, uint32_t block, const void* const* src, uint32_t n); /* engine.rs:159-175 */
+int sh_turbo_step(sh_turbo* t, uint32_t block, int direction, void* compute_stream);     /* engine.rs:304-341 */
+int sh_turbo_evict_sync(sh_turbo* t, uint32_t block, void* compute_stream);             /* lib.rs:68-73 */
+int sh_turbo_drain(sh_turbo* t);                                          /* lib.rs:108-118 */
+int sh_turbo_gpu_ptr(sh_turbo* t, uint32_t block, uint32_t param, uint64_t* ptr);       /* engine.rs:344-350 */
+int sh_turbo_cpu_ptr(sh_turbo* t, uint32_t block, uint32_t param, uint64_t* ptr);       /* engine.rs:353-358 */
+int sh_turbo_set_slot_gpu_ptrs(sh_turbo* t, uint32_t slot, const uint64_t* ptrs, uint32_t n); /* engine.rs:361-372 */
+/* No reference counterpart: a slot as one contiguous device buffer of at
+ * least sh_turbo_slot_bytes bytes; a block's param p then sits at its own
+ * aligned offset and the whole block is a single copy. */
+int sh_turbo_set_slot_buffer(sh_turbo* t, uint32_t slot, void* base, uint64_t bytes);
+int sh_turbo_slot_bytes(sh_turbo* t, uint64_t* bytes);
+int sh_turbo_param_offset(sh_turbo* t, uint32_t block, uint32_t param, uint64_t* offset);
+/* No reference counterpart (the reference always copies back): 0 skips the
+ * D2H at eviction for a block whose device copy is never written. */
+int sh_turbo_set_writeback(sh_turbo* t, uint32_t block, int enable);
+int sh_turbo_block_slot(sh_turbo* t, uint32_t block, int32_t* slot);     /* -1: none, engine.rs:375-378 */
+int sh_turbo_block_location(sh_turbo* t, uint32_t block, int* location); /* engine.rs:384-393 */
+int sh_turbo_counts(sh_turbo* t, uint32_t* blocks, uint32_t* slots, uint32_t* free_slots); /* engine.rs:380-382 */
+/* Bytes moved so far in each direction (telemetry; no reference counterpart). */
+int sh_turbo_bytes(sh_turbo* t, uint64_t* h2d, uint64_t* d2h);
+/* Timing of later H2D copies (no reference counterpart): with timing on, each
+ * block's latest H2D is bracketed by timing events; sh_turbo_block_times waits
+ * for it and returns its start and end in ms after `ref_event` (a timing event
+ * recorded earlier). */
+int sh_turbo_set_timing(sh_turbo* t, int enable);
+int sh_turbo_block_times(sh_turbo* t, uint32_t block, void* ref_event, float* out2);
+
 /* Host copy of the kernels' row-index division (floor(n[i] / d) through the
  * 64-bit multiplicative inverse stored in sh_unpack_desc.div_magic), exported
  * so the index arithmetic can be checked on a CPU. No reference counterpart. */

@@ -145,6 +145,27 @@ _SIGNATURES: dict[str, list] = {
     "sh_loader_release": [_vp, ctypes.c_uint64],
     "sh_loader_set_timing": [_vp, _i32],
     "sh_loader_ticket_times": [_vp, ctypes.c_uint64, _vp, _vp],
+    "sh_turbo_create": [ctypes.POINTER(_vp)],
+    "sh_turbo_destroy": [_vp],
+    "sh_turbo_register_block": [_vp, _vp, _u32, ctypes.POINTER(_u32)],
+    "sh_turbo_initialize": [_vp, _i32, _u32],
+    "sh_turbo_stage_block": [_vp, _u32, _vp, _u32],
+    "sh_turbo_step": [_vp, _u32, _i32, _vp],
+    "sh_turbo_evict_sync": [_vp, _u32, _vp],
+    "sh_turbo_drain": [_vp],
+    "sh_turbo_gpu_ptr": [_vp, _u32, _u32, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_turbo_cpu_ptr": [_vp, _u32, _u32, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_turbo_param_offset": [_vp, _u32, _u32, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_turbo_set_slot_gpu_ptrs": [_vp, _u32, _vp, _u32],
+    "sh_turbo_set_slot_buffer": [_vp, _u32, _vp, ctypes.c_uint64],
+    "sh_turbo_slot_bytes": [_vp, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_turbo_set_writeback": [_vp, _u32, _i32],
+    "sh_turbo_block_slot": [_vp, _u32, ctypes.POINTER(ctypes.c_int32)],
+    "sh_turbo_block_location": [_vp, _u32, ctypes.POINTER(_i32)],
+    "sh_turbo_counts": [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32), ctypes.POINTER(_u32)],
+    "sh_turbo_bytes": [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "sh_turbo_set_timing": [_vp, _i32],
+    "sh_turbo_block_times": [_vp, _u32, _vp, _vp],
 }
 
 # Mirror of `struct sh_load_request`.
