@@ -492,6 +492,103 @@ def turbo_leg(args) -> dict:
     return out
 
 
+def train_leg(args) -> dict:
+    """Config 5: one training step of a 48-block hidden-4096 DiT (17.8 B bf16 weights,
+    frozen, module-backed; LoRA rank 32 on the self-attention projections, trainable)
+    streamed through StagehandRuntime block mode under a 24 GB VRAM budget (watermarks
+    80 / 60 %), prefetch window 3, forward + backward hooks, activation checkpointing
+    per block, MSE loss, SGD on the LoRA weights. Run with the reference's eviction
+    (every parameter copied back to the host) and with frozen host copies (only the
+    trainable parameters copied back)."""
+    import gc
+
+    import torch
+
+    import stagehand_amd as stagehand
+    from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
+
+    g = torch.Generator(device="cuda").manual_seed(args.seed + 5)
+    x = torch.randn(1, 4096, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    ctx = torch.randn(1, 512, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    target = torch.randn(1, 4096, 4096, device="cuda", generator=g)
+    out = {"workload": "config5 48-block DiT (hidden 4096, 32 heads, MLP 4, self + cross attention, 17.77 B frozen "
+                       "bf16 block weights, LoRA r32 on self-attention q/k/v/o = 50.3 M trainable), batch 1 x 4096 "
+                       "tokens + 512 conditioning tokens, MSE loss, SGD on LoRA, activation checkpointing, "
+                       "VRAM budget 24 GB (watermarks 19200 / 14400 MB), prefetch window 3"}
+    for label, fhc in (("reference_eviction", False), ("frozen_host_copies", True)):
+        t0 = time.perf_counter()
+        with torch.device("meta"):
+            model = TrainDiT()
+        init_train_dit_(model, args.seed, device="cuda")
+        gen_s = time.perf_counter() - t0
+        cfg = stagehand.StagehandConfig(pinned_pool_mb=4096, pinned_slab_mb=256, vram_high_watermark_mb=19200,
+                                        vram_low_watermark_mb=14400, prefetch_window_blocks=3, max_inflight_transfers=4,
+                                        nan_inf_check=False, strict_bf16=False, telemetry_enabled=True,
+                                        frozen_host_copies=fhc)
+        cfg.telemetry_file = None
+        rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
+                                        inference_mode=False)
+        lora = [p for n, p in model.named_parameters() if "lora" in n]
+        opt = torch.optim.SGD(lora, lr=1e-3, foreach=False)
+        losses = []
+
+        def step(i: int) -> None:
+            xi = x.clone().requires_grad_()  # activations entering the blocks carry grad, as after an embedding
+            rt.begin_step(i)
+            with rt.managed_forward(), rt.managed_backward():
+                y = model(xi, ctx, vec)
+                loss = torch.nn.functional.mse_loss(y.float(), target)
+                loss.backward()
+            rt.end_step()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            losses.append(loss.detach())
+
+        for i in range(args.train_warmup):
+            step(i)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        h0, d0 = rt.engine.bytes_h2d, rt.engine.bytes_d2h
+        t1 = time.perf_counter()
+        for i in range(args.train_steps):
+            step(args.train_warmup + i)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t1
+        ms = wall / args.train_steps * 1e3
+        h2d = (rt.engine.bytes_h2d - h0) // args.train_steps
+        d2h = (rt.engine.bytes_d2h - d0) // args.train_steps
+        hist = rt.telemetry.history[-args.train_steps:]
+        rt.engine.start_trace()
+        step(args.train_warmup + args.train_steps)
+        trace = rt.engine.stop_trace()
+        timeline = timeline_stats(trace, getattr(args, "pcie_peak_gbps", None))
+        if trace["loads"]:
+            t_first = min(l[2] for l in trace["loads"])
+            timeline["load_gaps_ms_top"] = sorted(
+                (round(b[2] - a[3], 2) for a, b in zip(sorted(trace["loads"], key=lambda l: l[2]),
+                                                       sorted(trace["loads"], key=lambda l: l[2])[1:])),
+                reverse=True)[:8]
+            timeline["first_load_ms"] = round(t_first, 2)
+        res = {"ms_per_step": round(ms, 1), "h2d_bytes_per_step": h2d, "d2h_bytes_per_step": d2h, "timeline": timeline,
+               "h2d_gbps": round(h2d / (ms * 1e-3) / 1e9, 2), "d2h_gbps": round(d2h / (ms * 1e-3) / 1e9, 2),
+               "block_bytes": sum(e.size_bytes for e in rt.registry.blocks_in_order()),
+               "peak_vram_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+               "evictions_per_step": sum(m.evictions for m in hist) / len(hist),
+               "stall_ms_per_step": round(sum(m.stall_time_ms for m in hist) / len(hist), 1),
+               "losses": [round(float(v), 5) for v in losses], "weights_gen_s": round(gen_s, 1),
+               "steps": args.train_steps, "warmup": args.train_warmup}
+        out[label] = res
+        log(f"train/{label}: {res}")
+        rt.shutdown()
+        for e in rt.registry.blocks_in_order():
+            rt.residency.get_entry(e.block_id).gpu_tensor = None
+        del rt, model, opt, lora
+        gc.collect()
+        torch.cuda.empty_cache()
+    return out
+
+
 def dit_leg(kind: str, args) -> dict:
     """Streams the 19+38-block Flux-style DiT through StagehandRuntime block mode.
 
@@ -592,6 +689,9 @@ def main() -> int:
     ap.add_argument("--dit-modes", default="staged", choices=["staged", "pinned", "both"])
     ap.add_argument("--only-dit", action="store_true", help="skip the config-2 kernel legs (profiling the DiT stream)")
     ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
+    ap.add_argument("--train", default="on", choices=["on", "off"], help="config-5 streamed training step")
+    ap.add_argument("--train-steps", type=int, default=2)
+    ap.add_argument("--train-warmup", type=int, default=1)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -620,6 +720,8 @@ def main() -> int:
             out["dit_file"] = dit_leg("file", args)
         if args.turbo == "on":
             out["turbo"] = turbo_leg(args)
+        if args.train == "on":
+            out["train"] = train_leg(args)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -739,6 +841,9 @@ def main() -> int:
     if args.turbo == "on":
         log("turbo: config 3 DiT through the window engine")
         result["turbo"] = turbo_leg(args)
+    if args.train == "on":
+        log("train: config 5 streamed training step")
+        result["train"] = train_leg(args)
 
     print(json.dumps(result), flush=True)
     return 0

@@ -28,6 +28,20 @@ class StagehandConfig:
     # its first load, so later loads are a single DMA (no staging copy); costs
     # host memory equal to the streamed bytes of all such blocks
     pinned_source_cache: bool = False
+    # module-backed blocks: a frozen parameter (requires_grad False) whose host
+    # tensor already has the runtime dtype keeps that tensor while the block is
+    # resident, and eviction points the parameter back at it instead of copying
+    # the device copy back (the reference copies back every parameter,
+    # src/stagehand/scheduler.py:1216-1231, 1348-1366). Off by default: with it
+    # on, in-place writes to a frozen parameter on the device are dropped at
+    # eviction.
+    frozen_host_copies: bool = False
+    # the host waits in before_block until the compute of the block this many
+    # blocks back has finished on the device (0: never). Loads and waits are
+    # device-side, so without a bound the host can queue work for many blocks
+    # ahead of the device, and every evicted block still read by queued work
+    # keeps its memory; the reference blocks the host in every load instead.
+    max_run_ahead_blocks: int = 4
     # scheduling policy
     policy: str = "static"
     prefetch_window_blocks: int = 3

@@ -83,6 +83,7 @@ class StagehandRuntime:
         )
         self._vmm = None
         self._vmm_active_blocks: dict[str, int] = {}
+        self._recomputing: set[str] = set()
         log.info("StagehandRuntime: %d blocks registered, pool=%dMB, inference=%s", len(self._registry),
                  config.pinned_pool_mb, inference_mode)
 
@@ -117,13 +118,26 @@ class StagehandRuntime:
 
     # ── hooks ────────────────────────────────────────────────────────
 
+    # A forward of a block during the backward phase while its backward pre-hook
+    # holds it is an activation-checkpoint recompute: the block is already
+    # resident and referenced, and the recompute may stop before the block's
+    # forward returns (non-reentrant checkpointing stops once it has rebuilt the
+    # tensors it needs), so its forward post-hook may never run. Such forwards
+    # take no reference of their own; the backward post-hook ends them.
+
     def _make_pre_forward_hook(self, block_id: str):
         def hook(module: nn.Module, args: tuple) -> None:
+            if self._scheduler.in_backward_phase and self._residency.get_entry(block_id).refcount > 0:
+                self._recomputing.add(block_id)
+                return
             self._scheduler.before_block(block_id)
         return hook
 
     def _make_post_forward_hook(self, block_id: str):
         def hook(module: nn.Module, args: tuple, output: object) -> None:
+            if block_id in self._recomputing:
+                self._recomputing.discard(block_id)
+                return
             self._scheduler.after_block(block_id, _first_tensor(output))
         return hook
 
@@ -135,6 +149,7 @@ class StagehandRuntime:
 
     def _make_post_backward_hook(self, block_id: str):
         def hook(module: nn.Module, grad_input: tuple, grad_output: tuple) -> None:
+            self._recomputing.discard(block_id)
             self._scheduler.after_block(block_id)
         return hook
 
@@ -151,6 +166,7 @@ class StagehandRuntime:
             yield
         finally:
             self._scheduler.exit_backward_phase()
+            self._recomputing.clear()
             for h in handles:
                 h.remove()
 

@@ -23,6 +23,8 @@ and casts into CPU tensors); SquareQ dequantisation exists only on the device.
 """
 from __future__ import annotations
 
+import collections
+
 import logging
 import mmap
 import os
@@ -36,6 +38,7 @@ from torch import nn
 
 from stagehand_amd.residency import BlockState
 from stagehand_amd.staging import PlanCache, SourceBuilder, squareq_weight_tensors
+from stagehand_amd.transfer import NativeEvent
 
 if TYPE_CHECKING:
     from stagehand_amd.config import StagehandConfig
@@ -188,6 +191,11 @@ class StagehandScheduler:
         # block → event of the asynchronous D2H that moved its module parameters
         # to host memory at eviction; waited for before those tensors are read
         self._d2h_fences: dict[str, Any] = {}
+        # block → {param name: host tensor} kept for frozen module parameters while
+        # the block is resident (config.frozen_host_copies)
+        self._host_copies: dict[str, dict[str, torch.Tensor]] = {}
+        # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
+        self._done_marks: collections.deque = collections.deque()
 
     # ── step lifecycle ───────────────────────────────────────────────
 
@@ -214,6 +222,10 @@ class StagehandScheduler:
 
     def exit_backward_phase(self) -> None:
         self._backward_phase = False
+
+    @property
+    def in_backward_phase(self) -> bool:
+        return self._backward_phase
 
     def set_defer_backward_eviction(self, enabled: bool) -> None:
         self._defer_backward_eviction = enabled
@@ -257,6 +269,21 @@ class StagehandScheduler:
         if ev is not None:
             prev = self._d2h_fences.get(block_id)
             self._d2h_fences[block_id] = ev if prev is None else ev  # later event covers earlier copies on the stream
+
+    def _take_host_copies(self, block_id: str, module: nn.Module, names: list[str]) -> list[str]:
+        """Points frozen parameters kept with a host copy back at it; returns the names still to copy back."""
+        kept = self._host_copies.pop(block_id, None)
+        if not kept:
+            return names
+        params = dict(module.named_parameters())
+        rest = []
+        for name in names:
+            host = kept.get(name)
+            if host is not None and name in params and not params[name].requires_grad:
+                _set_param_data(module, name, host)
+            else:
+                rest.append(name)
+        return rest
 
     def _reconcile_file_backed_grads(self) -> None:
         for entry in self._ordered_blocks:
@@ -351,7 +378,20 @@ class StagehandScheduler:
 
     # ── per-block hooks ──────────────────────────────────────────────
 
+    def _bound_run_ahead(self) -> None:
+        """Host wait for the compute of the block ``max_run_ahead_blocks`` back."""
+        limit = getattr(self._config, "max_run_ahead_blocks", 0)
+        while limit > 0 and len(self._done_marks) >= limit:
+            self._done_marks.popleft().synchronize()
+
+    def _mark_block_done(self) -> None:
+        if self._has_cuda and getattr(self._config, "max_run_ahead_blocks", 0) > 0:
+            ev = NativeEvent()
+            ev.record(torch.cuda.current_stream().cuda_stream)
+            self._done_marks.append(ev)
+
     def before_block(self, block_id: str) -> None:
+        self._bound_run_ahead()
         self._engine._reap_d2h()  # release device buffers whose save-back copies finished
         state = self._residency.get_state(block_id)
         if state == BlockState.GPU_READY:
@@ -378,7 +418,12 @@ class StagehandScheduler:
                 log.warning("Hard stall on block %s (was %s): %.2f ms", block_id, state.value, stall_ms)
 
         self._residency.increment_ref(block_id)
-        self._residency.get_entry(block_id).last_used_step = self._current_step
+        entry = self._residency.get_entry(block_id)
+        entry.last_used_step = self._current_step
+        if self._has_cuda and entry.gpu_tensor is not None:
+            # block buffers come from the loader stream's pool (AsyncTransferEngine.alloc_device):
+            # register the compute stream's use so the memory is not reused before it has run
+            entry.gpu_tensor.record_stream(torch.cuda.current_stream())
         self._engine.mark_compute(block_id, start=True)
         self._cursor += 1
         if self._budget.above_high_watermark():
@@ -389,6 +434,7 @@ class StagehandScheduler:
 
     def after_block(self, block_id: str, output: torch.Tensor | None = None) -> None:
         self._engine.mark_compute(block_id, start=False)
+        self._mark_block_done()
         self._residency.decrement_ref(block_id)
         self._residency.get_entry(block_id).last_used_step = self._current_step
         if self._guards is not None and output is not None and self._config.nan_inf_check:
@@ -458,10 +504,15 @@ class StagehandScheduler:
         if state == BlockState.HOST_STAGED:
             if res_entry.gpu_tensor is None:
                 numel = block_entry.size_bytes // block_entry.dtype.itemsize
-                res_entry.gpu_tensor = torch.empty(numel, dtype=block_entry.dtype, device=self._device)
+                res_entry.gpu_tensor = (self._engine.alloc_device(numel, block_entry.dtype) if self._has_cuda else
+                                        torch.empty(numel, dtype=block_entry.dtype, device=self._device))
+                fresh = True
+            else:
+                fresh = False
             staged = res_entry.host_slab
             if self._has_cuda:
-                handle = self._engine.submit_block_load(block_id, staged, res_entry.gpu_tensor.view(torch.uint8))
+                handle = self._engine.submit_block_load(block_id, staged, res_entry.gpu_tensor.view(torch.uint8),
+                                                        dest_on_loader_stream=fresh)
                 res_entry.host_slab = None  # the loader owns slab staging and release
             else:
                 handle = self._engine.submit_h2d(block_id, staged, res_entry.gpu_tensor)
@@ -649,12 +700,23 @@ class StagehandScheduler:
         layout = _build_param_layout(module, block_entry.dtype)
         res_entry.param_layout = layout
         numel = block_entry.size_bytes // block_entry.dtype.itemsize
-        gpu_tensor = torch.empty(numel, dtype=block_entry.dtype, device=self._device)
+        gpu_tensor = (self._engine.alloc_device(numel, block_entry.dtype) if self._has_cuda else
+                      torch.empty(numel, dtype=block_entry.dtype, device=self._device))
         res_entry.gpu_tensor = gpu_tensor
         gpu_bytes = gpu_tensor.view(torch.uint8)
         if self._has_cuda:
             source = self._build_module_source(block_entry, module, layout)
-            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes)
+            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True)
+            if getattr(self._config, "frozen_host_copies", False):
+                params = dict(module.named_parameters())
+                keep = {}
+                for name, _shape, dtype, _off, numel in layout:
+                    p = params[name]
+                    if (not p.requires_grad and numel > 0 and p.data.device.type == "cpu" and p.data.dtype == dtype
+                            and p.data.is_contiguous()):
+                        keep[name] = p.data
+                if keep:
+                    self._host_copies[block_id] = keep
         else:
             _flatten_params_into_buffer(module, gpu_bytes, layout)
         _restore_params_from_tensor(module, gpu_bytes, layout)
@@ -738,8 +800,8 @@ class StagehandScheduler:
                 self._residency.transition(block_id, BlockState.EVICTING)
                 self._await_pending_load(block_id)
                 if module is not None:
-                    self._save_params_to_host(block_id, module, [n for n, _ in module.named_parameters()],
-                                              with_grads=True)
+                    names = self._take_host_copies(block_id, module, [n for n, _ in module.named_parameters()])
+                    self._save_params_to_host(block_id, module, names, with_grads=True)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -802,7 +864,8 @@ class StagehandScheduler:
         if module is not None and res_entry.param_layout is not None:
             if module_backed:
                 self._await_pending_load(block_id)
-                self._save_params_to_host(block_id, module, [n for n, *_ in res_entry.param_layout])
+                names = self._take_host_copies(block_id, module, [n for n, *_ in res_entry.param_layout])
+                self._save_params_to_host(block_id, module, names)
             elif block_entry.file_backed:  # SquareQ-backed blocks are file-backed too (registry BlockEntry.file_backed)
                 resident = set(block_entry.module_param_names)
                 keep_on_gpu = self._defer_backward_eviction and not self._backward_phase

@@ -138,6 +138,7 @@ class AsyncTransferEngine:
         self._inflight: list[TransferHandle] = []
         self._next_handle_id = 0
         self._loader = None
+        self._loader_stream = None
         self._owned_stream = None
         self._copy_stream = None
         self._copy_threads = copy_threads or min(16, os.cpu_count() or 1)
@@ -184,6 +185,24 @@ class AsyncTransferEngine:
         cs, us = ctypes.c_void_p(), ctypes.c_void_p()
         _native.call("sh_loader_streams", self._loader_handle(), ctypes.byref(cs), ctypes.byref(us))
         return cs.value, us.value
+
+    def _loader_copy_stream(self) -> torch.cuda.ExternalStream:
+        if self._loader_stream is None:
+            self._loader_stream = torch.cuda.ExternalStream(self.loader_streams()[0])
+        return self._loader_stream
+
+    def alloc_device(self, numel: int, dtype: torch.dtype) -> torch.Tensor:
+        """A destination buffer for block loads, allocated on the loader's copy stream.
+
+        torch's caching allocator hands a buffer freed on a stream back only to
+        allocations on the same stream, after the work queued there; buffers from
+        this pool are written by the loader's copy stream, so a load into one needs
+        no wait on the compute stream's queue. Compute use must be registered with
+        ``record_stream``, which keeps the memory from being handed out again until
+        that compute has run: callers call ``record_stream`` on the buffer for every
+        stream that uses it (the scheduler does so in ``before_block``)."""
+        with torch.cuda.stream(self._loader_copy_stream()):
+            return torch.empty(numel, dtype=dtype, device="cuda")
 
     # ── reference-compatible copies ──────────────────────────────────
 
@@ -233,8 +252,13 @@ class AsyncTransferEngine:
 
     # ── native block loads ───────────────────────────────────────────
 
-    def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor) -> TransferHandle:
-        """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path)."""
+    def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor,
+                          dest_on_loader_stream: bool = False) -> TransferHandle:
+        """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path).
+
+        The copy waits for the work queued on the current stream (``gpu_dest`` may reuse
+        memory that queued kernels still read) unless ``gpu_dest`` came from
+        ``alloc_device`` (``dest_on_loader_stream``)."""
         if not self._has_cuda:
             raise RuntimeError("submit_block_load needs a GPU")
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
@@ -266,15 +290,19 @@ class AsyncTransferEngine:
         req[0]["copy_threads"] = self._copy_threads
         req[0]["image"] = image
         if source.plan is not None:
-            staging = torch.empty(max(source.src_bytes, 1), dtype=torch.uint8, device=gpu_dest.device)
+            if dest_on_loader_stream:
+                with torch.cuda.stream(self._loader_copy_stream()):
+                    staging = torch.empty(max(source.src_bytes, 1), dtype=torch.uint8, device=gpu_dest.device)
+            else:
+                staging = torch.empty(max(source.src_bytes, 1), dtype=torch.uint8, device=gpu_dest.device)
             keep.append(staging)
             keep.append(source.plan)
             req[0]["plan"] = source.plan.handle.value
             req[0]["staging"] = staging.data_ptr()
             req[0]["staging_bytes"] = staging.numel()
         ticket = ctypes.c_uint64()
-        st = _native.lib().sh_loader_submit(self._loader_handle(), req.ctypes.data, _current_stream_handle(),
-                                            ctypes.byref(ticket))
+        wait_stream = self.loader_streams()[0] if dest_on_loader_stream else _current_stream_handle()
+        st = _native.lib().sh_loader_submit(self._loader_handle(), req.ctypes.data, wait_stream, ctypes.byref(ticket))
         if st != _native.SH_OK:
             self._raise_transfer(st, block_id, "load")
         handle.ticket = ticket.value

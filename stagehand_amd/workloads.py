@@ -207,3 +207,100 @@ def materialize_norms_(model: _nn.Module, device: str = "cpu") -> None:
     for mod in model.modules():
         if isinstance(mod, _nn.RMSNorm) and mod.weight is not None:
             mod.weight = _nn.Parameter(torch.ones(mod.weight.shape, device=device), requires_grad=False)
+
+
+# ── training DiT (config 5) ──────────────────────────────────────────────────
+
+
+class LoRALinear(_nn.Module):
+    """A frozen base Linear plus a trainable rank-r update: y = base(x) + (x Aᵀ) Bᵀ,
+    A ~ N(0, 0.01), B = 0 (so the adapter starts as the identity update)."""
+
+    def __init__(self, in_features: int, out_features: int, rank: int, bias: bool = True) -> None:
+        super().__init__()
+        self.base = _nn.Linear(in_features, out_features, bias=bias)
+        self.lora_A = _nn.Parameter(torch.empty(rank, in_features))
+        self.lora_B = _nn.Parameter(torch.zeros(out_features, rank))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.base(x) + _F.linear(_F.linear(x, self.lora_A), self.lora_B)
+
+
+class _Attn(_nn.Module):
+    def __init__(self, hidden: int, rank: int | None) -> None:
+        super().__init__()
+        make = (lambda: LoRALinear(hidden, hidden, rank)) if rank else (lambda: _nn.Linear(hidden, hidden))
+        self.q, self.k, self.v, self.o = make(), make(), make(), make()
+
+
+def _heads(x: torch.Tensor, heads: int) -> torch.Tensor:
+    b, s, h = x.shape
+    return x.view(b, s, heads, h // heads).transpose(1, 2)
+
+
+class TrainBlock(_nn.Module):
+    """WAN-style block: adaLN modulation, self-attention (LoRA on q/k/v/o),
+    cross-attention over a conditioning sequence, GELU MLP — 22·h² weights."""
+
+    def __init__(self, hidden: int, heads: int, mlp_ratio: float, rank: int) -> None:
+        super().__init__()
+        self.heads = heads
+        self.modulation = _nn.Linear(hidden, 6 * hidden)
+        self.self_attn = _Attn(hidden, rank)
+        self.cross_attn = _Attn(hidden, None)
+        mlp = int(hidden * mlp_ratio)
+        self.ffn = _nn.Sequential(_nn.Linear(hidden, mlp), _nn.GELU(approximate="tanh"), _nn.Linear(mlp, hidden))
+
+    def forward(self, x: torch.Tensor, ctx: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+        h, nh = x.shape[-1], self.heads
+        m = self.modulation(_F.silu(vec)[:, None, :]).chunk(6, dim=-1)
+        xn = _F.layer_norm(x, (h,), eps=1e-6) * (1 + m[1]) + m[0]
+        sa = self.self_attn
+        a = _attention(_heads(sa.q(xn), nh), _heads(sa.k(xn), nh), _heads(sa.v(xn), nh))
+        x = x + m[2] * sa.o(a.transpose(1, 2).reshape(x.shape))
+        ca = self.cross_attn
+        xn = _F.layer_norm(x, (h,), eps=1e-6)
+        a = _attention(_heads(ca.q(xn), nh), _heads(ca.k(ctx), nh), _heads(ca.v(ctx), nh))
+        x = x + ca.o(a.transpose(1, 2).reshape(x.shape))
+        return x + m[5] * self.ffn(_F.layer_norm(x, (h,), eps=1e-6) * (1 + m[4]) + m[3])
+
+
+class TrainDiT(_nn.Module):
+    """48 blocks, hidden 4096, 32 heads, MLP ratio 4, LoRA rank 32 on the self-attention
+    projections by default (17.7 B frozen block weights, 50 M trainable). Blocks are
+    recomputed in the backward pass (activation checkpointing) when ``checkpoint``."""
+
+    def __init__(self, depth: int = 48, hidden: int = 4096, heads: int = 32, mlp_ratio: float = 4.0, rank: int = 32,
+                 checkpoint: bool = True) -> None:
+        super().__init__()
+        self.checkpoint = checkpoint
+        self.blocks = _nn.ModuleList(TrainBlock(hidden, heads, mlp_ratio, rank) for _ in range(depth))
+
+    def forward(self, x: torch.Tensor, ctx: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+        from torch.utils.checkpoint import checkpoint
+
+        for blk in self.blocks:
+            if self.checkpoint and torch.is_grad_enabled():
+                x = checkpoint(blk, x, ctx, vec, use_reentrant=False)
+            else:
+                x = blk(x, ctx, vec)
+        return x
+
+
+TRAIN_BLOCK_PATTERN = r"^blocks\.\d+$"
+
+
+def init_train_dit_(model: TrainDiT, seed: int, device: str = "cpu") -> TrainDiT:
+    """bf16 weights: base N(0, 0.02), LoRA A N(0, 0.01), LoRA B 0 (drawn on ``device`` with a
+    seeded generator, then stored in host memory); base weights frozen, LoRA trainable."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    for mod in model.modules():
+        for name, prm in list(mod.named_parameters(recurse=False)):
+            if isinstance(mod, LoRALinear) and name == "lora_B":
+                t = torch.zeros(prm.shape, dtype=torch.bfloat16)
+            else:
+                std = 0.01 if (isinstance(mod, LoRALinear) and name == "lora_A") else 0.02
+                t = (torch.randn(prm.shape, device=device, generator=g) * std).to(torch.bfloat16).cpu()
+            trainable = isinstance(mod, LoRALinear)
+            setattr(mod, name, _nn.Parameter(t, requires_grad=trainable))
+    return model

@@ -285,3 +285,70 @@ def test_pinned_source_images_refresh_mutable_params(tmp_path):
     y2 = _run_blocks(rt2, model2, x, steps=1)[0]
     assert torch.equal(_bits(y1), _bits(y2))
     rt2.shutdown()
+
+
+def _train_dit(seed: int):
+    from stagehand_amd.workloads import TrainDiT, init_train_dit_
+
+    return init_train_dit_(TrainDiT(depth=4, hidden=128, heads=4, mlp_ratio=2.0, rank=8), seed)
+
+
+@pytest.mark.parametrize("frozen_host_copies", [False, True])
+def test_checkpointed_lora_training_round_trip(frozen_host_copies):
+    """Config-5 shape in small: frozen base weights, trainable LoRA, activation checkpointing
+    (blocks recomputed in backward under the runtime's hooks), module-backed eviction every
+    block, an SGD step on the LoRA parameters between steps. Outputs, LoRA gradients and the
+    updated LoRA weights match the same model trained unstreamed; with frozen host copies the
+    frozen weights are not copied back at eviction."""
+    from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN
+
+    model = _train_dit(5)
+    ref = _train_dit(5).cuda()
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(1, 32, 128, generator=g).to(torch.bfloat16).cuda()
+    ctx = torch.randn(1, 16, 128, generator=g).to(torch.bfloat16).cuda()
+    vec = torch.randn(1, 128, generator=g).to(torch.bfloat16).cuda()
+    target = torch.randn(1, 32, 128, generator=g).cuda()
+    base_mb = torch.cuda.memory_allocated() / 2**20
+    cfg = _config(vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb), prefetch_window_blocks=1,
+                  frozen_host_copies=frozen_host_copies)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
+                                    inference_mode=False)
+    lora = [p for n, p in model.named_parameters() if "lora" in n]
+    lora_ref = [p for n, p in ref.named_parameters() if "lora" in n]
+    opt = torch.optim.SGD(lora, lr=0.5, foreach=False)
+    opt_ref = torch.optim.SGD(lora_ref, lr=0.5, foreach=False)
+    for step in range(3):
+        xi = x.clone().requires_grad_()
+        rt.begin_step(step)
+        with rt.managed_forward(), rt.managed_backward():
+            y = model(xi, ctx, vec)
+            torch.nn.functional.mse_loss(y.float(), target).backward()
+        rt.end_step()
+        xr = x.clone().requires_grad_()
+        yr = ref(xr, ctx, vec)
+        torch.nn.functional.mse_loss(yr.float(), target).backward()
+        torch.cuda.synchronize()
+        assert torch.allclose(y.float(), yr.float(), atol=2e-2, rtol=2e-2), step
+        for (n, p), q in zip([(n, p) for n, p in model.named_parameters() if "lora" in n], lora_ref):
+            assert p.grad is not None, n
+            assert torch.allclose(p.grad.float().cpu(), q.grad.float().cpu(), atol=1e-3, rtol=5e-2), (step, n)
+        opt.step()
+        opt_ref.step()
+        opt.zero_grad(set_to_none=True)
+        opt_ref.zero_grad(set_to_none=True)
+    for (n, p), q in zip([(n, p) for n, p in model.named_parameters() if "lora" in n], lora_ref):
+        assert torch.allclose(p.float().cpu(), q.float().cpu(), atol=1e-2, rtol=5e-2), n
+    # every eviction of a block copies back its LoRA weights and gradients; without
+    # frozen host copies also its frozen weights
+    evictions = sum(m.evictions for m in rt.telemetry.history)
+    blk = ref.blocks[0]
+    frozen_per_block = sum(p.numel() * 2 for n, p in blk.named_parameters() if "lora" not in n)
+    lora_per_block = sum(p.numel() * 2 for n, p in blk.named_parameters() if "lora" in n)
+    sent_back = rt.engine.bytes_d2h
+    assert evictions > 0
+    if frozen_host_copies:
+        assert sent_back <= evictions * 2 * lora_per_block
+    else:
+        assert sent_back >= evictions * frozen_per_block
+    rt.shutdown()
