@@ -113,7 +113,8 @@ def copy_kernel_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
 
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
-    plan = UnpackPlan(make_descs([(KIND_COPY_BYTES, 0, 0, 1, nbytes, 0, 0)]))
+    half = nbytes // 2  # a region's length is a 32-bit field
+    plan = UnpackPlan(make_descs([(KIND_COPY_BYTES, 0, 0, 1, half, 0, 0), (KIND_COPY_BYTES, half, half, 1, half, 0, 0)]))
     stream = torch.cuda.current_stream()
     plan.run(a, b, stream=stream)
     torch.cuda.synchronize()

@@ -8,16 +8,17 @@
 //   zero-fill         src/stagehand/scheduler.py:240, 276-297, 325
 //
 // Work decomposition. Every descriptor covers rows*cols elements, cut into
-// tiles of kThreads * kUnroll * chunk elements; a host-built tile map gives
+// tiles of kThreads * unroll * chunk elements; a host-built tile map gives
 // each workgroup its descriptor in O(1) (one scalar load), and the descriptor
 // itself is a 64-byte scalar load, so all per-region state lives in SGPRs.
-// Each thread moves kUnroll chunks; all loads of a thread are issued before
-// the first conversion. Loads and stores are 128-bit (64-bit for the cast's
-// 8-byte output); the hardware's unaligned-access mode lets them start at any
-// byte offset, which the reference layout needs (it has no padding, so int8
-// regions start at arbitrary offsets). With int8 chunks of 16, every chunk of
-// a row whose length is a multiple of 16 needs one row scale, loaded once per
-// thread; shorter or ragged rows take an element-wise path. This is pure
+// Each thread moves `unroll` chunks; all loads of a thread are issued before
+// the first conversion. Loads and stores are up to 128-bit (an int8 chunk of
+// 8 is a 64-bit load and a 128-bit bf16 store; the cast reads 128 and writes
+// 64 bits); the hardware's unaligned-access mode lets them start at any byte
+// offset, which the reference layout needs (it has no padding, so int8 regions
+// start at arbitrary offsets). With int8 chunks of 8, every chunk of a row
+// whose length is a multiple of 8 needs one row scale, loaded once per chunk;
+// shorter or ragged rows take an element-wise path. This is pure
 // streaming: no LDS (the scale is one load per chunk) and no MFMA.
 //
 // Numerics. The dequant is computed exactly as the reference's torch CPU ops:
@@ -53,22 +54,41 @@ namespace {
 #ifndef SH_UNPACK_THREADS
 #define SH_UNPACK_THREADS 512
 #endif
-#ifndef SH_UNPACK_UNROLL
-#define SH_UNPACK_UNROLL 1
+#ifndef SH_UNROLL_I8
+#define SH_UNROLL_I8 2
+#endif
+#ifndef SH_UNROLL_F32
+#define SH_UNROLL_F32 1
 #endif
 #ifndef SH_CHUNK_I8
-#define SH_CHUNK_I8 16
+#define SH_CHUNK_I8 8
 #endif
 #ifndef SH_CHUNK_F32
 #define SH_CHUNK_F32 4
 #endif
 
 constexpr uint32_t kThreads = SH_UNPACK_THREADS;
-constexpr uint32_t kUnroll = SH_UNPACK_UNROLL;
+// Chunks per thread (lane-interleaved: chunk k of every lane of a wavefront is
+// one contiguous span). Measured on config 2 (512 threads): int8 chunks of 8
+// twice per thread 6.35 TB/s vs one chunk of 16 6.20 and two of 16 5.41; fp32
+// chunks of 4 once per thread 6.06 TB/s vs twice 5.70.
+constexpr uint32_t kUnrollI8 = SH_UNROLL_I8;
+constexpr uint32_t kUnrollF32 = SH_UNROLL_F32;
 constexpr uint32_t kChunkI8 = SH_CHUNK_I8;     // int8 elements per thread per chunk
 constexpr uint32_t kChunkF32 = SH_CHUNK_F32;   // fp32 elements per thread per chunk (cast)
 constexpr uint32_t kChunkB16 = 16;             // bf16 elements per thread per chunk (widen)
-constexpr uint32_t kChunkBytes = 64;           // bytes per thread per chunk (copy / zero)
+// Byte kinds, per thread per chunk (measured on a 4 GiB region: copy 16 B
+// 6.57 TB/s vs 32 B 5.90 and 64 B 5.30; zero fill 32 B 6.29 TB/s vs 16 B 5.08
+// and 64 B 5.76).
+#ifndef SH_CHUNK_COPY
+#define SH_CHUNK_COPY 16
+#endif
+#ifndef SH_CHUNK_ZERO
+#define SH_CHUNK_ZERO 32
+#endif
+constexpr uint32_t kChunkCopy = SH_CHUNK_COPY;
+constexpr uint32_t kChunkZero = SH_CHUNK_ZERO;
+static_assert(kChunkCopy % 16 == 0 && kChunkZero % 16 == 0, "byte chunks are whole 16-byte words");
 static_assert(kChunkI8 % 4 == 0 && kChunkF32 % 4 == 0, "chunks are whole 32-bit words");
 constexpr uint64_t kMaxDescElems = 1ull << 31;
 
@@ -76,9 +96,15 @@ constexpr uint32_t chunk_of(uint32_t kind) {
   return (kind == SH_KIND_I8_ROWSCALE_BF16 || kind == SH_KIND_I8_ROWSCALE_F32) ? kChunkI8
          : kind == SH_KIND_F32_BF16                                              ? kChunkF32
          : kind == SH_KIND_BF16_F32                                              ? kChunkB16
-                                                                                 : kChunkBytes;
+         : kind == SH_KIND_ZERO_BYTES                                            ? kChunkZero
+                                                                                 : kChunkCopy;
 }
-constexpr uint32_t tile_of(uint32_t kind) { return kThreads * kUnroll * chunk_of(kind); }
+constexpr uint32_t unroll_of(uint32_t kind) {
+  return (kind == SH_KIND_I8_ROWSCALE_BF16 || kind == SH_KIND_I8_ROWSCALE_F32) ? kUnrollI8
+         : kind == SH_KIND_F32_BF16                                              ? kUnrollF32
+                                                                                 : 1u;
+}
+constexpr uint32_t tile_of(uint32_t kind) { return kThreads * unroll_of(kind) * chunk_of(kind); }
 
 // NB bytes as 32-bit words; loaded and stored with unaligned-capable 128-bit
 // (or 64-bit) vector memory operations.
@@ -168,6 +194,7 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
                                         const float* __restrict__ scales,
                                         const float* __restrict__ zps, uint8_t* __restrict__ dst) {
   constexpr uint32_t C = kChunkI8;
+  constexpr uint32_t U = kUnrollI8;
   constexpr uint32_t kOutBytes = OUT_BF16 ? 2 : 4;
   const uint32_t cols = d.cols;
   const uint32_t numel = d.rows * cols;
@@ -176,19 +203,19 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
   uint8_t* o = dst + d.dst_off;
   const float* sc = scales + d.scale_off;
   const float* zp = HAS_ZP ? zps + d.scale_off : nullptr;
-  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
+  const uint32_t e0 = local * (kThreads * U * C) + threadIdx.x * C;
 
   if (ld == cols && (cols % C) == 0) {
     // Every chunk lies inside one row: one scale per chunk.
-    Words<C> q[kUnroll];
-    float sv[kUnroll], zv[kUnroll];
+    Words<C> q[U];
+    float sv[U], zv[U];
 #pragma unroll
-    for (uint32_t k = 0; k < kUnroll; ++k) {
+    for (uint32_t k = 0; k < U; ++k) {
       const uint32_t e = e0 + k * (kThreads * C);
       if (e < numel) q[k] = ldw<C>(s + e);
     }
 #pragma unroll
-    for (uint32_t k = 0; k < kUnroll; ++k) {
+    for (uint32_t k = 0; k < U; ++k) {
       const uint32_t e = e0 + k * (kThreads * C);
       if (e < numel) {
         const uint32_t r = sh::udiv(e, d.div_magic);
@@ -197,7 +224,7 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
       }
     }
 #pragma unroll
-    for (uint32_t k = 0; k < kUnroll; ++k) {
+    for (uint32_t k = 0; k < U; ++k) {
       const uint32_t e = e0 + k * (kThreads * C);
       if (e < numel) {
         uint8_t* out = o + (size_t)e * kOutBytes;
@@ -214,7 +241,7 @@ __device__ __forceinline__ void tile_i8(const sh_unpack_desc& d, uint32_t local,
   // Rows that are not a multiple of the chunk, or a padded source (ld > cols):
   // element-wise, with the row tracked incrementally inside each chunk.
 #pragma unroll 1
-  for (uint32_t k = 0; k < kUnroll; ++k) {
+  for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
     if (e >= numel) break;
     uint32_t r = sh::udiv(e, d.div_magic);
@@ -267,18 +294,19 @@ __device__ __forceinline__ void tile_f32_bf16(const sh_unpack_desc& d, uint32_t 
                                               const uint8_t* __restrict__ src,
                                               uint8_t* __restrict__ dst) {
   constexpr uint32_t C = kChunkF32;
+  constexpr uint32_t U = kUnrollF32;
   const uint32_t numel = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
-  Words<4 * C> v[kUnroll];
+  const uint32_t e0 = local * (kThreads * U * C) + threadIdx.x * C;
+  Words<4 * C> v[U];
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
+  for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
     if (e + C <= numel) v[k] = ldw<4 * C>(s + (size_t)e * 4);
   }
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
+  for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
     if (e + C <= numel) {
       Words<2 * C> ow;
@@ -303,18 +331,19 @@ __device__ __forceinline__ void tile_bf16_f32(const sh_unpack_desc& d, uint32_t 
                                               const uint8_t* __restrict__ src,
                                               uint8_t* __restrict__ dst) {
   constexpr uint32_t C = kChunkB16;
+  constexpr uint32_t U = 1;
   const uint32_t numel = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t e0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
-  Words<2 * C> v[kUnroll];
+  const uint32_t e0 = local * (kThreads * U * C) + threadIdx.x * C;
+  Words<2 * C> v[U];
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
+  for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
     if (e + C <= numel) v[k] = ldw<2 * C>(s + (size_t)e * 2);
   }
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
+  for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
     if (e + C <= numel) {
       Words<4 * C> ow;
@@ -341,29 +370,35 @@ template <bool ZERO>
 __device__ __forceinline__ void tile_bytes(const sh_unpack_desc& d, uint32_t local,
                                            const uint8_t* __restrict__ src,
                                            uint8_t* __restrict__ dst) {
-  constexpr uint32_t C = kChunkBytes;
+  // A tile is kThreads * U * C bytes, moved as 16-byte words with
+  // consecutive lanes on consecutive words (each load / store instruction of a
+  // wavefront covers one contiguous 1 KiB span).
+  constexpr uint32_t C = ZERO ? kChunkZero : kChunkCopy;
+  constexpr uint32_t U = 1;
+  constexpr uint32_t W = 16;
+  constexpr uint32_t kWords = U * (C / W);
   const uint32_t nbytes = d.rows * d.cols;
   const uint8_t* s = src + d.src_off;
   uint8_t* o = dst + d.dst_off;
-  const uint32_t b0 = local * (kThreads * kUnroll * C) + threadIdx.x * C;
-  Words<C> v[kUnroll];
+  const uint32_t t0 = local * (kThreads * U * C);
+  Words<W> v[kWords];
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t b = b0 + k * (kThreads * C);
-    if (b + C <= nbytes) {
+  for (uint32_t k = 0; k < kWords; ++k) {
+    const uint32_t b = t0 + (k * kThreads + threadIdx.x) * W;
+    if (b + W <= nbytes) {
       if (ZERO) {
 #pragma unroll
-        for (uint32_t w = 0; w < C / 4; ++w) v[k].w[w] = 0;
+        for (uint32_t w = 0; w < W / 4; ++w) v[k].w[w] = 0;
       } else {
-        v[k] = ldw<C>(s + b);
+        v[k] = ldw<W>(s + b);
       }
     }
   }
 #pragma unroll
-  for (uint32_t k = 0; k < kUnroll; ++k) {
-    const uint32_t b = b0 + k * (kThreads * C);
-    if (b + C <= nbytes) {
-      stw<C>(o + b, v[k]);
+  for (uint32_t k = 0; k < kWords; ++k) {
+    const uint32_t b = t0 + (k * kThreads + threadIdx.x) * W;
+    if (b + W <= nbytes) {
+      stw<W>(o + b, v[k]);
     } else if (b < nbytes) {
       for (uint32_t j = b; j < nbytes; ++j) o[j] = ZERO ? (uint8_t)0 : s[j];
     }
