@@ -341,6 +341,94 @@ int sh_turbo_bytes(sh_turbo* t, uint64_t* h2d, uint64_t* d2h);
 int sh_turbo_set_timing(sh_turbo* t, int enable);
 int sh_turbo_block_times(sh_turbo* t, uint32_t block, void* ref_event, float* out2);
 
+/* ───────────────────────── VMM residency allocator ─────────────────────────
+ * Slabs of reserved device address space whose regions get physical memory on
+ * demand (hipMemCreate / hipMemMap / hipMemSetAccess) and lose it under a VRAM
+ * ceiling: the HIP rewrite of the reference's SlabAllocator
+ * (vmm_src/allocator.rs:75-713, eviction.rs:15-144, handle.rs:65-110,
+ * prefetch.rs, Python surface vmm_src/python.rs:39-267). Thread-safe; a
+ * Resident region is served with atomics only. Region offsets must be
+ * multiples of the granularity and regions must fit their slab
+ * (SH_ERR_INVALID otherwise).
+ * Errors (vmm_src/error.rs:30-53): Watermarked / NoEvictableRegions →
+ * SH_ERR_WATERMARK (MemoryError); invalid slab / region → SH_ERR_INVALID
+ * (ValueError); slab with live handles, released handle → SH_ERR_STATE
+ * (RuntimeError); HIP failures → SH_ERR_HIP (RuntimeError). */
+enum sh_vmm_region_state { SH_VMM_UNMAPPED = 0, SH_VMM_MAPPED_EMPTY = 1, SH_VMM_RESIDENT = 2 }; /* slab.rs:9-20 */
+typedef struct sh_vmm sh_vmm;
+typedef struct sh_vmm_handle sh_vmm_handle;
+typedef struct sh_vmm_stats {  /* python.rs:97-106 */
+  uint64_t total_slabs;
+  uint64_t total_regions;
+  uint64_t mapped_bytes;
+  uint64_t vram_ceiling;
+  uint64_t granularity;
+  /* counters (no reference counterpart) */
+  uint64_t maps;
+  uint64_t evictions;
+  uint64_t unmap_failures;
+  uint64_t last_unmap_error;  /* hipError_t of the last failed unmap */
+} sh_vmm_stats;
+typedef struct sh_vmm_region_stats {  /* allocator.rs:51-58 */
+  uint32_t state;
+  uint32_t refcount;
+  uint64_t offset;
+  uint64_t size;
+  uint64_t last_access;
+  uint64_t watermark;  /* of the region's slab */
+  uint32_t priority;   /* of the region's slab */
+  uint32_t reserved;
+} sh_vmm_region_stats;
+/* ceiling_bytes 0: total VRAM - max(2 GB, 15 %) (allocator.rs:111-115). */
+int sh_vmm_create(int device, uint64_t ceiling_bytes, sh_vmm** out);            /* allocator.rs:80-137 */
+/* The allocator's memory is released once every handle is released too. */
+int sh_vmm_destroy(sh_vmm* v);                                                  /* allocator.rs:648-713 */
+int sh_vmm_info(sh_vmm* v, sh_vmm_stats* stats);                                /* allocator.rs:591-646 */
+int sh_vmm_create_slab(sh_vmm* v, uint64_t size, uint32_t* slab);               /* allocator.rs:140-172 */
+int sh_vmm_define_region(sh_vmm* v, uint32_t slab, uint64_t offset, uint64_t size, uint32_t* region); /* :175-198 */
+int sh_vmm_ensure_resident(sh_vmm* v, uint32_t slab, uint32_t region, void* stream, sh_vmm_handle** out); /* :213-468 */
+int sh_vmm_prefetch(sh_vmm* v, uint32_t slab, uint32_t region);                 /* allocator.rs:470-503 */
+int sh_vmm_set_priority(sh_vmm* v, uint32_t slab, uint32_t priority);          /* allocator.rs:505-533 */
+int sh_vmm_set_ceiling(sh_vmm* v, uint64_t ceiling_bytes);                      /* allocator.rs:535-537 */
+int sh_vmm_destroy_slab(sh_vmm* v, uint32_t slab);                              /* allocator.rs:539-585 */
+int sh_vmm_region_info(sh_vmm* v, uint32_t slab, uint32_t region, sh_vmm_region_stats* stats);
+int sh_vmm_handle_ptr(sh_vmm_handle* h, void** ptr);                            /* handle.rs:36-44 */
+/* Mapping generation of the region when the handle was taken; it changes at
+ * every (re)map, after which the region holds no data (no reference
+ * counterpart: the reference's populate-once flag survives an eviction,
+ * vmm_backend.py:205-208). */
+int sh_vmm_handle_generation(sh_vmm_handle* h, uint64_t* generation);
+/* Records an event on the handle's stream, then drops its reference
+ * (handle.rs:65-110); SH_ERR_STATE when already released (python.rs:225-233). */
+int sh_vmm_handle_release(sh_vmm_handle* h);
+int sh_vmm_handle_destroy(sh_vmm_handle* h);  /* releases if needed, frees the handle */
+
+/* DLPack (the open tensor-exchange ABI, DLManagedTensor layout) with the ROCm
+ * device type, replacing vmm_src/dlpack.rs:4-76 (kDLCUDA). The exported tensor
+ * holds its own reference to the region until its deleter runs
+ * (python.rs:137-221). */
+#define SH_DL_ROCM 10
+typedef struct { int32_t device_type; int32_t device_id; } sh_dl_device;
+typedef struct { uint8_t code; uint8_t bits; uint16_t lanes; } sh_dl_dtype;
+typedef struct {
+  void* data;
+  sh_dl_device device;
+  int32_t ndim;
+  sh_dl_dtype dtype;
+  int64_t* shape;
+  int64_t* strides;
+  uint64_t byte_offset;
+} sh_dl_tensor;
+typedef struct sh_dl_managed_tensor {
+  sh_dl_tensor dl_tensor;
+  void* manager_ctx;
+  void (*deleter)(struct sh_dl_managed_tensor* self);
+} sh_dl_managed_tensor;
+int sh_vmm_handle_export(sh_vmm_handle* h, uint8_t code, uint8_t bits, int32_t ndim, const int64_t* shape,
+                         sh_dl_managed_tensor** out);
+/* Runs the deleter of an export that was never consumed. */
+int sh_dl_free(sh_dl_managed_tensor* t);
+
 /* Host copy of the kernels' row-index division (floor(n[i] / d) through the
  * 64-bit multiplicative inverse stored in sh_unpack_desc.div_magic), exported
  * so the index arithmetic can be checked on a CPU. No reference counterpart. */

@@ -165,6 +165,23 @@ _SIGNATURES: dict[str, list] = {
     "sh_turbo_counts": [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32), ctypes.POINTER(_u32)],
     "sh_turbo_bytes": [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
     "sh_turbo_set_timing": [_vp, _i32],
+    "sh_vmm_create": [_i32, ctypes.c_uint64, ctypes.POINTER(_vp)],
+    "sh_vmm_destroy": [_vp],
+    "sh_vmm_info": [_vp, _vp],
+    "sh_vmm_create_slab": [_vp, ctypes.c_uint64, ctypes.POINTER(_u32)],
+    "sh_vmm_define_region": [_vp, _u32, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(_u32)],
+    "sh_vmm_ensure_resident": [_vp, _u32, _u32, _vp, ctypes.POINTER(_vp)],
+    "sh_vmm_prefetch": [_vp, _u32, _u32],
+    "sh_vmm_set_priority": [_vp, _u32, _u32],
+    "sh_vmm_set_ceiling": [_vp, ctypes.c_uint64],
+    "sh_vmm_destroy_slab": [_vp, _u32],
+    "sh_vmm_region_info": [_vp, _u32, _u32, _vp],
+    "sh_vmm_handle_ptr": [_vp, ctypes.POINTER(_vp)],
+    "sh_vmm_handle_generation": [_vp, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_vmm_handle_release": [_vp],
+    "sh_vmm_handle_destroy": [_vp],
+    "sh_vmm_handle_export": [_vp, ctypes.c_uint8, ctypes.c_uint8, ctypes.c_int32, _vp, ctypes.POINTER(_vp)],
+    "sh_dl_free": [_vp],
     "sh_turbo_block_times": [_vp, _u32, _vp, _vp],
 }
 
@@ -180,6 +197,13 @@ POOL_STATS_DTYPE = np.dtype([
     ("total", "<u8"), ("free", "<u8"), ("in_use", "<u8"), ("peak_in_use", "<u8"), ("wait_count", "<u8"),
     ("fenced", "<u8"), ("total_wait_ms", "<f8"), ("slab_bytes", "<u8"), ("pinned", "<u8"),
 ])
+
+# Mirrors of `struct sh_vmm_stats` / `struct sh_vmm_region_stats`.
+VMM_STATS_DTYPE = np.dtype([("total_slabs", "<u8"), ("total_regions", "<u8"), ("mapped_bytes", "<u8"),
+                            ("vram_ceiling", "<u8"), ("granularity", "<u8"), ("maps", "<u8"), ("evictions", "<u8"),
+                            ("unmap_failures", "<u8"), ("last_unmap_error", "<u8")])
+VMM_REGION_DTYPE = np.dtype([("state", "<u4"), ("refcount", "<u4"), ("offset", "<u8"), ("size", "<u8"),
+                             ("last_access", "<u8"), ("watermark", "<u8"), ("priority", "<u4"), ("reserved", "<u4")])
 
 # Mirror of `struct sh_copy_item`.
 COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])

@@ -81,9 +81,25 @@ class StagehandRuntime:
                                          eviction_cooldown_steps=config.eviction_cooldown_steps),
             guards=self._guards, telemetry=self._telemetry, config=config, inference_mode=inference_mode,
         )
+        # VMM backend (inference only, as src/stagehand/__init__.py:185-198): blocks
+        # registered with vmm_register_model are served from mapped device memory
         self._vmm = None
+        self._vmm_model_id: str | None = None
         self._vmm_active_blocks: dict[str, int] = {}
+        self._vmm_block_id_to_idx: dict[str, int] = {}
         self._recomputing: set[str] = set()
+        self._vmm_saved: dict[str, list] = {}
+        if inference_mode and torch.cuda.is_available():
+            from stagehand_amd import vmm as _vmm_mod
+
+            if _vmm_mod.is_available():
+                try:
+                    self._vmm = _vmm_mod.VmmManager(device=torch.cuda.current_device(), engine=self._engine)
+                    for i, entry in enumerate(self._registry.blocks_in_order()):
+                        self._vmm_block_id_to_idx[entry.block_id] = i
+                except Exception as e:  # noqa: BLE001 — the block-swap path still works
+                    log.warning("VMM init failed, using block-swap: %s", e)
+                    self._vmm = None
         log.info("StagehandRuntime: %d blocks registered, pool=%dMB, inference=%s", len(self._registry),
                  config.pinned_pool_mb, inference_mode)
 
@@ -116,6 +132,114 @@ class StagehandRuntime:
         log.info("StagehandRuntime: converted %d params to sharded file-backed source (%s)", n, source_dir)
         return n
 
+    # ── VMM (src/stagehand/__init__.py:278-448) ──────────────────────
+
+    def vmm_register_model(self, model_id: str, dtype_str: str = "bfloat16", safetensors_path: str | None = None):
+        """Registers every block with the VMM backend (one region per block). Weights come from
+        ``safetensors_path`` (fully-qualified parameter names) or, without one, from host copies of
+        the module parameters. Returns the VmmModelHandle, or None without the backend."""
+        if self._vmm is None:
+            return None
+        ordered = self._registry.blocks_in_order()
+        handle = self._vmm.register_model(model_id, [e.size_bytes for e in ordered], dtype_str)
+        for i, entry in enumerate(ordered):
+            layout = self._block_layout(entry)
+            total = sum(numel for *_r, numel in layout)
+            if total > 0:
+                handle.register_block_shape(i, [total])
+        source_ok = False
+        if safetensors_path is not None and str(safetensors_path).endswith(".safetensors"):
+            names_by_module = {id(m): n for n, m in self._model.named_modules()}
+            block_map = []
+            for entry in ordered:
+                module = entry.module_ref()
+                prefix = names_by_module.get(id(module), "") if module is not None else ""
+                prefix = prefix + "." if prefix else ""
+                block_map.append([prefix + name for name, *_r in self._block_layout(entry)])
+            try:
+                handle.set_mmap_source(str(safetensors_path), block_map)
+                source_ok = True
+            except Exception as e:  # noqa: BLE001
+                log.warning("VMM: file source failed for %s: %s, falling back to host copies", model_id, e)
+        if not source_ok:
+            for i, entry in enumerate(ordered):
+                module = entry.module_ref()
+                layout = self._block_layout(entry)
+                if module is None or not layout:
+                    continue
+                params = dict(module.named_parameters())
+                parts = [params[name].data.to(dtype).reshape(-1).view(torch.uint8) for name, _s, dtype, _o, _n in layout
+                         if params[name].numel() > 0]
+                if parts:
+                    handle.set_ram_weights(i, torch.cat(parts).cpu())
+        self._vmm.activate_model(model_id)
+        self._vmm_model_id = model_id
+        log.info("VMM: registered model %s with %d blocks", model_id, len(ordered))
+        return handle
+
+    def _block_layout(self, entry) -> list:
+        if entry.param_layout:
+            return list(entry.param_layout)
+        module = entry.module_ref()
+        if module is None:
+            return []
+        from stagehand_amd.scheduler import _build_param_layout
+
+        return _build_param_layout(module, entry.dtype)
+
+    def _vmm_before_block(self, block_id: str, module: nn.Module) -> bool:
+        """Serves the block from its VMM region; False sends it down the block-swap path."""
+        if self._vmm is None or self._vmm_model_id not in self._vmm.models:
+            return False
+        idx = self._vmm_block_id_to_idx.get(block_id)
+        if idx is None:
+            return False
+        handle = self._vmm.models[self._vmm_model_id]
+        handle.prefetch_block(idx + 1)
+        tensor, ok = handle.get_block_tensor(idx, torch.cuda.current_stream().cuda_stream)
+        if not ok:
+            return False
+        try:
+            layout = self._block_layout(self._registry.get(block_id))
+            if layout:
+                from stagehand_amd.scheduler import _get_param_data, _restore_params_from_tensor
+
+                # what the parameters hold now (host tensors of module-resident parameters,
+                # the block-swap copy's views, or empty placeholders) comes back after the block
+                self._vmm_saved[block_id] = [(name, _get_param_data(module, name)) for name, *_r in layout]
+                _restore_params_from_tensor(module, tensor.view(torch.uint8), layout)
+        except Exception as e:  # noqa: BLE001
+            log.warning("VMM: param restore failed for %s, falling back: %s", block_id, e)
+            handle.release_block(idx)
+            return False
+        self._vmm_active_blocks[block_id] = idx
+        self._scheduler._cursor += 1
+        self._telemetry.record_prefetch_hit()
+        self._scheduler._prefetch_ahead()
+        return True
+
+    def _vmm_after_block(self, block_id: str) -> None:
+        idx = self._vmm_active_blocks.pop(block_id, None)
+        if idx is None:
+            return
+        entry = self._registry.get(block_id)
+        module = entry.module_ref()
+        saved = self._vmm_saved.pop(block_id, None)
+        if module is not None and saved:
+            # the parameter views hold the region's tensor: give the parameters back what
+            # they held before the block (the reference empties them, which loses
+            # module-resident parameters such as norms and the block-swap copy's views)
+            from stagehand_amd.scheduler import _set_param_data
+
+            for name, data in saved:
+                _set_param_data(module, name, data)
+        if self._vmm_model_id in self._vmm.models:
+            self._vmm.models[self._vmm_model_id].release_block(idx)
+
+    @property
+    def vmm(self):
+        return self._vmm
+
     # ── hooks ────────────────────────────────────────────────────────
 
     # A forward of a block during the backward phase while its backward pre-hook
@@ -130,6 +254,8 @@ class StagehandRuntime:
             if self._scheduler.in_backward_phase and self._residency.get_entry(block_id).refcount > 0:
                 self._recomputing.add(block_id)
                 return
+            if self._vmm is not None and self._vmm_before_block(block_id, module):
+                return
             self._scheduler.before_block(block_id)
         return hook
 
@@ -137,6 +263,9 @@ class StagehandRuntime:
         def hook(module: nn.Module, args: tuple, output: object) -> None:
             if block_id in self._recomputing:
                 self._recomputing.discard(block_id)
+                return
+            if block_id in self._vmm_active_blocks:
+                self._vmm_after_block(block_id)
                 return
             self._scheduler.after_block(block_id, _first_tensor(output))
         return hook
@@ -196,6 +325,11 @@ class StagehandRuntime:
     def shutdown(self) -> None:
         if _DEBUG_SHUTDOWN:
             print("[stagehand/debug] runtime.shutdown: engine drain start", flush=True)
+        if self._vmm is not None:
+            for bid in list(self._vmm_active_blocks):
+                self._vmm_after_block(bid)
+            self._vmm.shutdown()
+            self._vmm = None
         self._engine.shutdown()
         self._scheduler.close()
         self._pool.shutdown()

@@ -1,0 +1,459 @@
+"""VMM residency backend: block weights in device virtual memory that is mapped
+on demand and unmapped under a VRAM ceiling.
+
+``SlabAllocator`` / ``ResidentHandle`` are the Python face of the reference's
+pyo3 classes (vmm_src/python.rs:39-267) over the native allocator
+(``sh_vmm_*`` in include/stagehand_native.h): same methods, arguments and
+exception types (MemoryError when a region is watermarked or nothing can be
+evicted, ValueError for a bad slab / region / dtype, RuntimeError for a
+released handle or a slab with live handles). ``as_tensor`` exports the region
+through DLPack with the ROCm device type; the tensor keeps its own reference to
+the region.
+
+``VmmModelHandle`` / ``VmmManager`` / ``is_available`` follow
+src/stagehand/vmm_backend.py:21-440: one slab per model, one region per block,
+weights populated on first use from a safetensors file or from host tensors.
+Differences: regions start at granularity multiples (the reference places them
+at running byte offsets); a block is re-populated whenever its region has been
+re-mapped since it was filled (the reference's populate-once flag survives an
+eviction, vmm_backend.py:205-208); the file is read through this package's
+safetensors parser and ``mmap`` (the reference uses an external reader), and
+with an ``AsyncTransferEngine`` the fill is a native block load (pinned
+staging, copy stream) that the compute stream waits for on the device.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import mmap
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+import torch
+
+from stagehand_amd import _native
+from stagehand_amd._native import VMM_REGION_DTYPE, VMM_STATS_DTYPE
+
+__all__ = ["SlabAllocator", "ResidentHandle", "VmmModelHandle", "VmmManager", "is_available", "RegionState"]
+
+log = logging.getLogger(__name__)
+
+
+class RegionState:
+    UNMAPPED = 0
+    MAPPED_EMPTY = 1
+    RESIDENT = 2
+
+
+# DLPack (code, bits) per dtype name (vmm_src/dlpack.rs:66-76); float8 is exported as
+# uint8 bytes and viewed as float8 on the torch side.
+_DL_DTYPES: dict[str, tuple[int, int, torch.dtype]] = {
+    "float32": (2, 32, torch.float32),
+    "float16": (2, 16, torch.float16),
+    "bfloat16": (4, 16, torch.bfloat16),
+    "int8": (0, 8, torch.int8),
+    "int32": (0, 32, torch.int32),
+    "int64": (0, 64, torch.int64),
+    "uint8": (1, 8, torch.uint8),
+    "float8_e4m3fn": (1, 8, torch.float8_e4m3fn),
+}
+
+_capsule_new = ctypes.pythonapi.PyCapsule_New
+_capsule_new.restype = ctypes.py_object
+_capsule_new.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
+
+_available: bool | None = None
+
+
+def is_available() -> bool:
+    """True when the native library is built and device 0 supports virtual memory management."""
+    global _available
+    if _available is not None:
+        return _available
+    try:
+        if not torch.cuda.is_available():
+            _available = False
+            return False
+        h = ctypes.c_void_p()
+        st = _native.lib().sh_vmm_create(torch.cuda.current_device(), 0, ctypes.byref(h))
+        if st == _native.SH_OK:
+            _native.lib().sh_vmm_destroy(h)
+        _available = st == _native.SH_OK
+    except _native.NativeLibraryError:
+        _available = False
+    return _available
+
+
+class SlabAllocator:
+    """Native VMM allocator (vmm_src/python.rs:39-110)."""
+
+    def __init__(self, device: int = 0, ceiling_mb: Optional[int] = None) -> None:
+        h = ctypes.c_void_p()
+        _native.call("sh_vmm_create", int(device), 0 if ceiling_mb is None else int(ceiling_mb) << 20, ctypes.byref(h))
+        self._h = h
+        self.device = int(device)
+
+    def _handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise RuntimeError("VMM allocator has been closed")
+        return self._h
+
+    def create_slab(self, total_size: int) -> int:
+        out = ctypes.c_uint32()
+        _native.call("sh_vmm_create_slab", self._handle(), int(total_size), ctypes.byref(out))
+        return out.value
+
+    def define_region(self, slab: int, offset: int, size: int) -> int:
+        out = ctypes.c_uint32()
+        _native.call("sh_vmm_define_region", self._handle(), int(slab), int(offset), int(size), ctypes.byref(out))
+        return out.value
+
+    def ensure_resident(self, slab: int, region: int, stream: int) -> "ResidentHandle":
+        """Maps the region if needed; ``stream`` is the consumer's stream handle
+        (``torch.cuda.current_stream().cuda_stream``)."""
+        out = ctypes.c_void_p()
+        _native.call("sh_vmm_ensure_resident", self._handle(), int(slab), int(region), int(stream), ctypes.byref(out))
+        return ResidentHandle(out, self)
+
+    def prefetch(self, slab: int, region: int) -> None:
+        _native.call("sh_vmm_prefetch", self._handle(), int(slab), int(region))
+
+    def set_priority(self, slab: int, priority: int) -> None:
+        _native.call("sh_vmm_set_priority", self._handle(), int(slab), int(priority))
+
+    def set_vram_ceiling(self, ceiling_bytes: int) -> None:
+        _native.call("sh_vmm_set_ceiling", self._handle(), int(ceiling_bytes))
+
+    def destroy_slab(self, slab: int) -> None:
+        _native.call("sh_vmm_destroy_slab", self._handle(), int(slab))
+
+    def stats(self) -> dict:
+        st = np.zeros(1, dtype=VMM_STATS_DTYPE)
+        _native.call("sh_vmm_info", self._handle(), st.ctypes.data)
+        return {k: int(st[0][k]) for k in VMM_STATS_DTYPE.names}
+
+    def granularity(self) -> int:
+        return self.stats()["granularity"]
+
+    def region_stats(self, slab: int, region: int) -> dict:
+        st = np.zeros(1, dtype=VMM_REGION_DTYPE)
+        _native.call("sh_vmm_region_info", self._handle(), int(slab), int(region), st.ctypes.data)
+        return {k: int(st[0][k]) for k in VMM_REGION_DTYPE.names if k != "reserved"}
+
+    def close(self) -> None:
+        """Stops the prefetch worker; device memory goes once every handle is released."""
+        if self._h is not None:
+            _native.lib().sh_vmm_destroy(self._h)
+            self._h = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ResidentHandle:
+    """Keeps a region mapped while held (vmm_src/python.rs:111-267)."""
+
+    def __init__(self, handle: ctypes.c_void_p, allocator: SlabAllocator) -> None:
+        self._h = handle
+        self._alloc = allocator  # keeps the Python allocator object alive while handles exist
+
+    @property
+    def released(self) -> bool:
+        return self._h is None
+
+    def data_ptr(self) -> int:
+        if self._h is None:
+            raise RuntimeError("Handle already released")
+        out = ctypes.c_void_p()
+        _native.call("sh_vmm_handle_ptr", self._h, ctypes.byref(out))
+        return out.value
+
+    def generation(self) -> int:
+        """Mapping generation of the region: it changes at every (re)map, which loses the contents."""
+        if self._h is None:
+            raise RuntimeError("Handle already released")
+        out = ctypes.c_uint64()
+        _native.call("sh_vmm_handle_generation", self._h, ctypes.byref(out))
+        return out.value
+
+    def as_tensor(self, dtype: str, shape: list[int]) -> torch.Tensor:
+        """A device tensor over the region (DLPack); it keeps the region mapped until it is freed."""
+        if self._h is None:
+            raise RuntimeError("Handle already released")
+        if dtype not in _DL_DTYPES:
+            raise ValueError(f"Unsupported dtype: {dtype}")
+        code, bits, tdtype = _DL_DTYPES[dtype]
+        dims = np.ascontiguousarray(shape, dtype=np.int64)
+        managed = ctypes.c_void_p()
+        _native.call("sh_vmm_handle_export", self._h, code, bits, dims.size, dims.ctypes.data, ctypes.byref(managed))
+        try:
+            capsule = _capsule_new(managed, b"dltensor", None)
+            t = torch.utils.dlpack.from_dlpack(capsule)
+        except Exception:
+            _native.lib().sh_dl_free(managed)  # the export was not consumed
+            raise
+        return t.view(tdtype) if t.dtype != tdtype else t
+
+    def release(self) -> None:
+        if self._h is None:
+            raise RuntimeError("Handle already released")
+        h, self._h = self._h, None
+        _native.lib().sh_vmm_handle_destroy(h)
+
+    def __del__(self) -> None:
+        try:
+            if self._h is not None:
+                h, self._h = self._h, None
+                _native.lib().sh_vmm_handle_destroy(h)
+        except Exception:
+            pass
+
+
+# ── model handles (src/stagehand/vmm_backend.py:86-440) ──────────────────
+
+
+class VmmModelHandle:
+    """One slab per model, one region per block (vmm_backend.py:86-359)."""
+
+    def __init__(self, allocator: SlabAllocator, model_id: str, block_sizes: list[int], dtype: str,
+                 engine=None) -> None:
+        self.allocator = allocator
+        self.model_id = model_id
+        self.dtype = dtype
+        self.block_count = len(block_sizes)
+        self.block_sizes = list(block_sizes)
+        self._engine = engine
+        gran = allocator.granularity()
+        self._offsets = []
+        offset = 0
+        for size in block_sizes:
+            self._offsets.append(offset)
+            offset += -(-max(size, 1) // gran) * gran
+        self.slab_id = allocator.create_slab(max(offset, gran))
+        self.regions = [allocator.define_region(self.slab_id, off, max(size, 1))
+                        for off, size in zip(self._offsets, block_sizes)]
+        self.block_shapes: list[list[int] | None] = [None] * self.block_count
+        self._active_handles: dict[int, ResidentHandle] = {}
+        self._filled_generation: list[int | None] = [None] * self.block_count
+        self._current_priority = 0
+        self._destroyed = False
+        self._file = None  # (file object, mmap, memoryview)
+        self._block_pieces: list[list[tuple[int, int, int]]] = []  # per block: (dst offset, file offset, bytes)
+        self._ram_weight_refs: list[torch.Tensor | None] = [None] * self.block_count
+
+    def register_block_shape(self, block_idx: int, shape: list[int]) -> None:
+        self.block_shapes[block_idx] = list(shape)
+
+    # ── weight sources ───────────────────────────────────────────────
+
+    def set_mmap_source(self, safetensors_path: str, block_tensor_map: list[list[str]]) -> None:
+        """Weights come from ``safetensors_path``: for each block, the named tensors back to back."""
+        from stagehand_amd.registry import parse_safetensors_index
+
+        index = parse_safetensors_index(Path(safetensors_path))
+        pieces = []
+        for names in block_tensor_map:
+            dst, blk = 0, []
+            for name in names:
+                if name not in index:
+                    raise KeyError(f"{name!r} is not in {safetensors_path}")
+                off, nbytes = index[name][0], index[name][1]
+                blk.append((dst, off, nbytes))
+                dst += nbytes
+            pieces.append(blk)
+        fh = open(safetensors_path, "rb")
+        mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        self._close_file()
+        self._file = (fh, mm, memoryview(mm))
+        self._block_pieces = pieces
+        self._filled_generation = [None] * self.block_count
+
+    def set_ram_weights(self, block_idx: int, weights: torch.Tensor) -> None:
+        self._ram_weight_refs[block_idx] = weights
+
+    def _close_file(self) -> None:
+        if self._file is not None:
+            fh, mm, view = self._file
+            for fn in (view.release, mm.close, fh.close):
+                try:
+                    fn()
+                except Exception:
+                    pass
+            self._file = None
+
+    # ── block access ─────────────────────────────────────────────────
+
+    def get_block_tensor(self, block_idx: int, stream: int) -> tuple[torch.Tensor | None, bool]:
+        """(tensor, True), or (None, False) when the region is watermarked (vmm_backend.py:190-222)."""
+        if self.block_shapes[block_idx] is None:
+            raise RuntimeError(f"Block {block_idx} shape not registered. Call register_block_shape first.")
+        handle = None
+        try:
+            handle = self.allocator.ensure_resident(self.slab_id, self.regions[block_idx], stream)
+            tensor = handle.as_tensor(self.dtype, self.block_shapes[block_idx])
+            gen = handle.generation()
+            if self._filled_generation[block_idx] != gen:
+                self._populate_block(block_idx, tensor)
+                self._filled_generation[block_idx] = gen
+            self._active_handles[block_idx] = handle
+            return tensor, True
+        except MemoryError:
+            if handle is not None:
+                handle.release()
+            return None, False
+        except Exception:
+            if handle is not None and not handle.released:
+                handle.release()
+            raise
+
+    def _host_pieces(self, block_idx: int) -> list[tuple[int, torch.Tensor]]:
+        if self._file is not None and block_idx < len(self._block_pieces):
+            view = self._file[2]
+            return [(dst, torch.frombuffer(view, dtype=torch.uint8, count=n, offset=off))
+                    for dst, off, n in self._block_pieces[block_idx] if n > 0]
+        ram = self._ram_weight_refs[block_idx]
+        if ram is not None:
+            return [(0, ram.detach().reshape(-1).contiguous().view(torch.uint8))]
+        raise RuntimeError(f"No weight source for block {block_idx}")
+
+    def _populate_block(self, block_idx: int, vmm_tensor: torch.Tensor) -> None:
+        dst = vmm_tensor.view(-1).view(torch.uint8)
+        pieces = self._host_pieces(block_idx)
+        if self._engine is not None and torch.cuda.is_available():
+            from stagehand_amd.transfer import BlockSource
+
+            src_bytes = max((off + t.numel() for off, t in pieces), default=0)
+            handle = self._engine.submit_block_load(f"{self.model_id}:{block_idx}", BlockSource(pieces, src_bytes),
+                                                    dst[:src_bytes])
+            self._engine.wait_device(handle)
+        else:
+            for off, t in pieces:
+                dst[off:off + t.numel()].copy_(t, non_blocking=True)
+
+    def prefetch_block(self, block_idx: int) -> None:
+        """Maps the block's region ahead on the allocator's worker and warms the file pages."""
+        if not 0 <= block_idx < self.block_count:
+            return
+        try:
+            self.allocator.prefetch(self.slab_id, self.regions[block_idx])
+        except Exception:
+            pass
+        if self._file is not None and block_idx < len(self._block_pieces):
+            blk = self._block_pieces[block_idx]
+            if blk:
+                start = min(off for _d, off, _n in blk)
+                end = max(off + n for _d, off, n in blk)
+                try:
+                    page = mmap.PAGESIZE
+                    self._file[1].madvise(mmap.MADV_WILLNEED, start // page * page, end - start // page * page)
+                except (AttributeError, OSError, ValueError):
+                    pass
+
+    # ── lifecycle ────────────────────────────────────────────────────
+
+    def release_block(self, block_idx: int) -> None:
+        handle = self._active_handles.pop(block_idx, None)
+        if handle is not None and not handle.released:
+            handle.release()
+
+    def set_priority(self, priority: int) -> None:
+        self._current_priority = priority
+        self.allocator.set_priority(self.slab_id, priority)
+
+    def invalidate_weights(self) -> None:
+        self._filled_generation = [None] * self.block_count
+
+    def release_all(self) -> None:
+        for idx in list(self._active_handles):
+            self.release_block(idx)
+
+    def release_mmap(self) -> None:
+        """Lets the OS drop the file's pages (they are re-read on the next fill)."""
+        if self._file is not None:
+            try:
+                self._file[1].madvise(mmap.MADV_DONTNEED)
+            except (AttributeError, OSError):
+                pass
+
+    def destroy(self) -> None:
+        if self._destroyed:
+            return
+        self._destroyed = True
+        self.release_all()
+        self._ram_weight_refs = [None] * self.block_count
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()  # fills may still read the file's pages
+        if self._engine is not None:
+            self._engine.drain()
+        self._close_file()
+        try:
+            self.allocator.destroy_slab(self.slab_id)
+        except Exception as e:
+            log.warning("VMM: destroy_slab failed for %s: %s", self.model_id, e)
+
+    def __del__(self) -> None:
+        if self._destroyed:
+            return
+        if self._active_handles:
+            log.warning("VMM: %s dropped with %d active handles; slab kept", self.model_id, len(self._active_handles))
+            return
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class VmmManager:
+    """The allocator and its per-model handles (vmm_backend.py:365-440)."""
+
+    def __init__(self, device: int = 0, ceiling_mb: Optional[int] = None, engine=None) -> None:
+        if not is_available():
+            raise RuntimeError("VMM backend not available")
+        self.allocator = SlabAllocator(device=device, ceiling_mb=ceiling_mb)
+        self.models: dict[str, VmmModelHandle] = {}
+        self._priority_counter = 0
+        self._engine = engine
+        s = self.allocator.stats()
+        log.info("VMM: allocator ready. ceiling=%.2fGB, granularity=%.1fMB", s["vram_ceiling"] / 1e9,
+                 s["granularity"] / 1e6)
+
+    def register_model(self, model_id: str, block_sizes: list[int], dtype: str) -> VmmModelHandle:
+        if model_id in self.models:
+            log.warning("VMM: %s already registered, replacing", model_id)
+            self.models[model_id].destroy()
+        handle = VmmModelHandle(self.allocator, model_id, block_sizes, dtype, engine=self._engine)
+        self.models[model_id] = handle
+        return handle
+
+    def activate_model(self, model_id: str) -> None:
+        if model_id not in self.models:
+            return
+        self._priority_counter += 1
+        self.models[model_id].set_priority(self._priority_counter)
+        for mid, handle in self.models.items():
+            if mid != model_id:
+                handle.release_mmap()
+
+    def unregister_model(self, model_id: str) -> None:
+        handle = self.models.pop(model_id, None)
+        if handle is not None:
+            handle.destroy()
+
+    def set_ceiling(self, ceiling_bytes: int) -> None:
+        self.allocator.set_vram_ceiling(ceiling_bytes)
+
+    def stats(self) -> dict:
+        s = self.allocator.stats()
+        mm = sum(len(h._file[1]) for h in self.models.values() if h._file is not None)
+        s["mmap_data_bytes"] = mm
+        s["mmap_data_gb"] = round(mm / 1e9, 2)
+        return s
+
+    def shutdown(self) -> None:
+        for mid in list(self.models):
+            self.unregister_model(mid)
+        self.allocator.close()
