@@ -590,6 +590,79 @@ def train_leg(args) -> dict:
     return out
 
 
+def _vmm_run(args, src: Path) -> dict:
+    """Config-3 DiT served from the VMM backend: every block registered in one slab,
+    filled from the sharded safetensors on first use (native loads), then resident
+    in mapped device memory under the default ceiling."""
+    import gc
+
+    import torch
+
+    import stagehand_amd as stagehand
+    from stagehand_amd.workloads import DIT_BLOCK_PATTERN
+
+    model = _dit_model()
+    rt = stagehand.StagehandRuntime(model, _dit_config("file", args, False), block_pattern=DIT_BLOCK_PATTERN,
+                                    dtype=torch.bfloat16, inference_mode=True)
+    rt.convert_registry_to_file_backed_sharded(str(src))
+    handle = rt.vmm_register_model("dit", "bfloat16", str(src))
+    if handle is None:
+        rt.shutdown()
+        return {"skipped": "VMM backend unavailable"}
+    img, txt, vec = _dit_inputs(args.seed)
+    served = {"vmm": 0, "swap": 0}
+    orig = rt._vmm_before_block
+
+    def counted(bid, module):
+        ok = orig(bid, module)
+        served["vmm" if ok else "swap"] += 1
+        return ok
+
+    rt._vmm_before_block = counted
+
+    def step(i: int):
+        rt.begin_step(i)
+        with torch.no_grad(), rt.managed_forward():
+            out = model(img, txt, vec)
+        rt.end_step()
+        return out
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step(0)
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    for i in range(args.dit_warmup):
+        step(1 + i)
+    torch.cuda.synchronize()
+    served = {"vmm": 0, "swap": 0}
+    t1 = time.perf_counter()
+    for i in range(args.dit_steps):
+        out = step(1 + args.dit_warmup + i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t1) / args.dit_steps * 1e3
+    # fast path: ensure_resident + release of a resident region, through the Python binding
+    alloc = rt.vmm.allocator
+    stream = torch.cuda.current_stream().cuda_stream
+    n = 2000
+    t2 = time.perf_counter()
+    for _ in range(n):
+        alloc.ensure_resident(handle.slab_id, handle.regions[0], stream).release()
+    fast_us = (time.perf_counter() - t2) / n * 1e6
+    st = rt.vmm.stats()
+    res = {"first_step_ms": round(first_ms, 1), "ms_per_step": round(ms, 2), "steps": args.dit_steps,
+           "blocks_served_per_step": {k: v / args.dit_steps for k, v in served.items()},
+           "mapped_gb": round(st["mapped_bytes"] / 1e9, 2), "vram_ceiling_gb": round(st["vram_ceiling"] / 1e9, 1),
+           "granularity": st["granularity"], "maps": st["maps"], "evictions": st["evictions"],
+           "ensure_release_fast_path_us": round(fast_us, 2), "out_finite": bool(torch.isfinite(out.float()).all())}
+    log(f"dit/vmm: {res}")
+    rt.shutdown()
+    del rt, model, out
+    gc.collect()
+    torch.cuda.empty_cache()
+    return res
+
+
 def dit_leg(kind: str, args) -> dict:
     """Streams the 19+38-block Flux-style DiT through StagehandRuntime block mode.
 
@@ -629,6 +702,9 @@ def dit_leg(kind: str, args) -> dict:
               "scale_rows", "peak_vram_gb"):
         res[k] = best[k]
     res["best_mode"] = best["source_mode"]
+    if kind == "file" and args.vmm == "on":
+        log("dit/file: served from the VMM backend")
+        res["vmm"] = _vmm_run(args, src)
     shutil.rmtree(workdir, ignore_errors=True)
     return res
 
@@ -691,6 +767,7 @@ def main() -> int:
     ap.add_argument("--only-dit", action="store_true", help="skip the config-2 kernel legs (profiling the DiT stream)")
     ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
     ap.add_argument("--train", default="on", choices=["on", "off"], help="config-5 streamed training step")
+    ap.add_argument("--vmm", default="on", choices=["on", "off"], help="config-3 DiT served from the VMM backend")
     ap.add_argument("--train-steps", type=int, default=2)
     ap.add_argument("--train-warmup", type=int, default=1)
     args = ap.parse_args()

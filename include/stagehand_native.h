@@ -349,7 +349,10 @@ int sh_turbo_block_times(sh_turbo* t, uint32_t block, void* ref_event, float* ou
  * prefetch.rs, Python surface vmm_src/python.rs:39-267). Thread-safe; a
  * Resident region is served with atomics only. Region offsets must be
  * multiples of the granularity and regions must fit their slab
- * (SH_ERR_INVALID otherwise).
+ * (SH_ERR_INVALID otherwise). Each region reserves its own address range (a
+ * slab groups its regions and bounds their offsets; regions of one slab are not
+ * contiguous in address space): on gfx950, hipMemSetAccess refuses a mapping
+ * inside a reservation that already holds a mapping of another size.
  * Errors (vmm_src/error.rs:30-53): Watermarked / NoEvictableRegions →
  * SH_ERR_WATERMARK (MemoryError); invalid slab / region → SH_ERR_INVALID
  * (ValueError); slab with live handles, released handle → SH_ERR_STATE

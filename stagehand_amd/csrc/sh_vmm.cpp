@@ -23,11 +23,16 @@
 //    (allocator.rs:505-533); a handle's release records an event on its stream
 //    before dropping its reference (handle.rs:65-110);
 //  * prefetch maps a region on a worker thread (prefetch.rs).
-// Differences: the access clock and per-region last access are atomics (the
-// reference's try_lock stamping can leave hot regions unstamped); a region must
-// start at a granularity multiple and end inside its slab (checked when it is
-// defined instead of failing at map time); mapping is synchronous on the host,
-// so a prefetch needs no event; DLPack export uses kDLROCM.
+// Differences: every region reserves its own address range when it is defined
+// (a slab is the group of its regions and bounds their offsets) — on gfx950
+// with ROCm 7.2, hipMemSetAccess refuses (invalid argument) a mapping inside a
+// reservation that already holds a mapping of another size, while separate
+// reservations map any mix of sizes; the access clock and per-region last
+// access are atomics (the reference's try_lock stamping can leave hot regions
+// unstamped); a region must start at a granularity multiple and end inside its
+// slab (checked when it is defined instead of failing at map time); mapping is
+// synchronous on the host, so a prefetch needs no event; DLPack export uses
+// kDLROCM.
 #include <algorithm>
 #include <atomic>
 #include <condition_variable>
@@ -45,6 +50,7 @@ namespace {
 enum : uint8_t { kUnmapped = SH_VMM_UNMAPPED, kResident = SH_VMM_RESIDENT };
 
 struct VRegion {
+  void* base = nullptr;  // the region's own address reservation
   uint64_t offset = 0, size = 0;
   std::atomic<uint8_t> state{kUnmapped};
   std::atomic<uint32_t> refcount{0};
@@ -58,7 +64,6 @@ struct VRegion {
 };
 
 struct VSlab {
-  void* base = nullptr;
   uint64_t size = 0;
   std::vector<std::unique_ptr<VRegion>> regions;
   std::atomic<uint32_t> priority{0};
@@ -101,12 +106,25 @@ namespace {
 
 uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
-void unmap_region(VSlab& s, VRegion& r) {
+void unmap_region(VRegion& r) {
   std::lock_guard<std::mutex> g(r.mu);
   if (r.has_phys) {
-    (void)hipMemUnmap(static_cast<uint8_t*>(s.base) + r.offset, r.size);
+    (void)hipMemUnmap(r.base, r.size);
     (void)hipMemRelease(r.phys);
     r.has_phys = false;
+  }
+}
+
+void free_region(VRegion& r) {
+  if (r.last_use) {
+    (void)hipEventSynchronize(r.last_use);
+    (void)hipEventDestroy(r.last_use);
+    r.last_use = nullptr;
+  }
+  unmap_region(r);
+  if (r.base) {
+    (void)hipMemAddressFree(r.base, r.size);
+    r.base = nullptr;
   }
 }
 
@@ -114,14 +132,7 @@ void free_everything(sh_vmm* v) {
   (void)hipSetDevice(v->device);
   for (auto& sp : v->slabs) {
     if (!sp) continue;
-    for (auto& rp : sp->regions) {
-      if (rp->last_use) {
-        (void)hipEventSynchronize(rp->last_use);
-        (void)hipEventDestroy(rp->last_use);
-      }
-      unmap_region(*sp, *rp);
-    }
-    (void)hipMemAddressFree(sp->base, sp->size);
+    for (auto& rp : sp->regions) free_region(*rp);
   }
   v->slabs.clear();
 }
@@ -134,10 +145,10 @@ void drop_ref(sh_vmm* v) {
 }
 
 // Caller holds cold_mu and a shared lock on slabs_mu.
-int map_region(sh_vmm* v, VSlab& s, VRegion& r) {
+int map_region(sh_vmm* v, VRegion& r) {
   hipMemGenericAllocationHandle_t h{};
   SH_HIP(hipMemCreate(&h, r.size, &v->prop, 0));
-  void* p = static_cast<uint8_t*>(s.base) + r.offset;
+  void* p = r.base;
   hipError_t e = hipMemMap(p, r.size, 0, h, 0);
   if (e != hipSuccess) {
     (void)hipMemRelease(h);
@@ -203,7 +214,7 @@ int evict_for_space(sh_vmm* v, uint64_t needed) {
       if (r.last_use && r.last_use_recorded) (void)hipEventSynchronize(r.last_use);
       r.last_use_recorded = false;
       if (r.has_phys) {
-        hipError_t e = hipMemUnmap(static_cast<uint8_t*>(s.base) + r.offset, r.size);
+        hipError_t e = hipMemUnmap(r.base, r.size);
         if (e != hipSuccess) {
           v->unmap_failures++;
           v->last_unmap_error = (int)e;
@@ -256,7 +267,7 @@ void prefetch_one(sh_vmm* v, uint32_t slab, uint32_t region) {
   if (region >= s->watermark.load(std::memory_order_acquire)) return;
   if (r->state.load(std::memory_order_acquire) == kResident) return;
   if (evict_for_space(v, r->size) != SH_OK) { sh::clear_error(); return; }
-  if (map_region(v, *s, *r) != SH_OK) sh::clear_error();
+  if (map_region(v, *r) != SH_OK) sh::clear_error();
 }
 
 void worker_loop(sh_vmm* v) {
@@ -338,13 +349,8 @@ extern "C" int sh_vmm_create_slab(sh_vmm* v, uint64_t size, uint32_t* slab) {
   sh::clear_error();
   if (!v || !slab) return sh::fail(SH_ERR_INVALID, "sh_vmm_create_slab: null argument");
   if (size == 0) return sh::fail(SH_ERR_INVALID, "slab size must be positive");
-  const uint64_t rounded = round_up(size, v->granularity);
-  SH_HIP(hipSetDevice(v->device));
-  void* base = nullptr;
-  SH_HIP(hipMemAddressReserve(&base, rounded, v->granularity, nullptr, 0));
   auto s = std::make_unique<VSlab>();
-  s->base = base;
-  s->size = rounded;
+  s->size = round_up(size, v->granularity);
   std::unique_lock<std::shared_mutex> g(v->slabs_mu);
   for (size_t i = 0; i < v->slabs.size(); ++i) {
     if (!v->slabs[i]) {
@@ -376,7 +382,12 @@ extern "C" int sh_vmm_define_region(sh_vmm* v, uint32_t slab, uint64_t offset, u
   r->offset = offset;
   r->size = rounded;
   SH_HIP(hipSetDevice(v->device));
-  SH_HIP(hipEventCreateWithFlags(&r->last_use, hipEventDisableTiming));
+  SH_HIP(hipMemAddressReserve(&r->base, rounded, v->granularity, nullptr, 0));
+  hipError_t e = hipEventCreateWithFlags(&r->last_use, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    (void)hipMemAddressFree(r->base, rounded);
+    return sh::fail(SH_ERR_HIP, "HIP error %d (%s) in hipEventCreateWithFlags", (int)e, hipGetErrorString(e));
+  }
   s.regions.push_back(std::move(r));
   if (s.watermark.load() == 0) s.watermark.store(s.regions.size());
   *region = (uint32_t)(s.regions.size() - 1);
@@ -399,7 +410,7 @@ extern "C" int sh_vmm_ensure_resident(sh_vmm* v, uint32_t slab, uint32_t region,
       r->refcount.fetch_add(1, std::memory_order_acq_rel);
       if (r->state.load(std::memory_order_acquire) == kResident) {
         r->last_access.store(v->clock.fetch_add(1) + 1, std::memory_order_relaxed);
-        *out = make_handle(v, slab, region, static_cast<uint8_t*>(s->base) + r->offset, st, r->generation.load());
+        *out = make_handle(v, slab, region, r->base, st, r->generation.load());
         return SH_OK;
       }
       r->refcount.fetch_sub(1, std::memory_order_acq_rel);  // lost to an eviction
@@ -422,12 +433,12 @@ extern "C" int sh_vmm_ensure_resident(sh_vmm* v, uint32_t slab, uint32_t region,
       if (region < wm) s->watermark.store(region, std::memory_order_release);
       return sh::fail(SH_ERR_WATERMARK, "Region watermarked — use fallback path");
     }
-    rc = map_region(v, *s, *r);
+    rc = map_region(v, *r);
     if (rc != SH_OK) return rc;
   }
   r->refcount.fetch_add(1, std::memory_order_acq_rel);
   r->last_access.store(v->clock.fetch_add(1) + 1, std::memory_order_relaxed);
-  *out = make_handle(v, slab, region, static_cast<uint8_t*>(s->base) + r->offset, st, r->generation.load());
+  *out = make_handle(v, slab, region, r->base, st, r->generation.load());
   return SH_OK;
 }
 
@@ -480,16 +491,10 @@ extern "C" int sh_vmm_destroy_slab(sh_vmm* v, uint32_t slab) {
     if (r->refcount.load() > 0) return sh::fail(SH_ERR_STATE, "Slab has active handles");
   SH_HIP(hipSetDevice(v->device));
   for (auto& r : s.regions) {
-    if (r->last_use) {
-      (void)hipEventSynchronize(r->last_use);
-      (void)hipEventDestroy(r->last_use);
-      r->last_use = nullptr;
-    }
     if (r->state.load() == kResident) v->mapped_bytes -= r->size;
-    unmap_region(s, *r);
+    free_region(*r);
     r->state.store(kUnmapped);
   }
-  SH_HIP(hipMemAddressFree(s.base, s.size));
   v->slabs[slab].reset();
   return SH_OK;
 }

@@ -15,6 +15,7 @@ from __future__ import annotations
 import logging
 import os
 from contextlib import contextmanager
+from pathlib import Path
 from typing import Generator
 
 import torch
@@ -136,8 +137,9 @@ class StagehandRuntime:
 
     def vmm_register_model(self, model_id: str, dtype_str: str = "bfloat16", safetensors_path: str | None = None):
         """Registers every block with the VMM backend (one region per block). Weights come from
-        ``safetensors_path`` (fully-qualified parameter names) or, without one, from host copies of
-        the module parameters. Returns the VmmModelHandle, or None without the backend."""
+        ``safetensors_path`` — a file, or a directory of shards with its index (fully-qualified
+        parameter names) — or, without one, from host copies of the module parameters. Returns
+        the VmmModelHandle, or None without the backend."""
         if self._vmm is None:
             return None
         ordered = self._registry.blocks_in_order()
@@ -148,7 +150,8 @@ class StagehandRuntime:
             if total > 0:
                 handle.register_block_shape(i, [total])
         source_ok = False
-        if safetensors_path is not None and str(safetensors_path).endswith(".safetensors"):
+        if safetensors_path is not None and (str(safetensors_path).endswith(".safetensors")
+                                             or Path(safetensors_path).is_dir()):
             names_by_module = {id(m): n for n, m in self._model.named_modules()}
             block_map = []
             for entry in ordered:

@@ -241,8 +241,8 @@ class VmmModelHandle:
         self._filled_generation: list[int | None] = [None] * self.block_count
         self._current_priority = 0
         self._destroyed = False
-        self._file = None  # (file object, mmap, memoryview)
-        self._block_pieces: list[list[tuple[int, int, int]]] = []  # per block: (dst offset, file offset, bytes)
+        self._files: dict[str, tuple] = {}  # path → (file object, mmap, memoryview)
+        self._block_pieces: list[list[tuple[int, str, int, int]]] = []  # per block: (dst off, file, file off, bytes)
         self._ram_weight_refs: list[torch.Tensor | None] = [None] * self.block_count
 
     def register_block_shape(self, block_idx: int, shape: list[int]) -> None:
@@ -251,24 +251,40 @@ class VmmModelHandle:
     # ── weight sources ───────────────────────────────────────────────
 
     def set_mmap_source(self, safetensors_path: str, block_tensor_map: list[list[str]]) -> None:
-        """Weights come from ``safetensors_path``: for each block, the named tensors back to back."""
+        """Weights come from ``safetensors_path`` — one file, or a directory of shards with a
+        ``*.safetensors.index.json`` — for each block, the named tensors back to back."""
+        import json
+
         from stagehand_amd.registry import parse_safetensors_index
 
-        index = parse_safetensors_index(Path(safetensors_path))
+        src = Path(safetensors_path)
+        where: dict[str, tuple[str, int, int]] = {}  # tensor → (file, offset, bytes)
+        if src.is_dir():
+            idx = next((src / n for n in ("diffusion_pytorch_model.safetensors.index.json",
+                                          "model.safetensors.index.json") if (src / n).exists()), None)
+            if idx is None:
+                raise FileNotFoundError(f"No safetensors index found in {src}")
+            for shard in dict.fromkeys(json.loads(idx.read_text())["weight_map"].values()):
+                for k, meta in parse_safetensors_index(src / shard).items():
+                    where[k] = (str(src / shard), meta[0], meta[1])
+        else:
+            for k, meta in parse_safetensors_index(src).items():
+                where[k] = (str(src), meta[0], meta[1])
         pieces = []
         for names in block_tensor_map:
             dst, blk = 0, []
             for name in names:
-                if name not in index:
+                if name not in where:
                     raise KeyError(f"{name!r} is not in {safetensors_path}")
-                off, nbytes = index[name][0], index[name][1]
-                blk.append((dst, off, nbytes))
+                path, off, nbytes = where[name]
+                blk.append((dst, path, off, nbytes))
                 dst += nbytes
             pieces.append(blk)
-        fh = open(safetensors_path, "rb")
-        mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
         self._close_file()
-        self._file = (fh, mm, memoryview(mm))
+        for path in dict.fromkeys(p for blk in pieces for _d, p, _o, _n in blk):
+            fh = open(path, "rb")
+            mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+            self._files[path] = (fh, mm, memoryview(mm))
         self._block_pieces = pieces
         self._filled_generation = [None] * self.block_count
 
@@ -276,14 +292,13 @@ class VmmModelHandle:
         self._ram_weight_refs[block_idx] = weights
 
     def _close_file(self) -> None:
-        if self._file is not None:
-            fh, mm, view = self._file
+        for fh, mm, view in self._files.values():
             for fn in (view.release, mm.close, fh.close):
                 try:
                     fn()
                 except Exception:
                     pass
-            self._file = None
+        self._files = {}
 
     # ── block access ─────────────────────────────────────────────────
 
@@ -311,10 +326,9 @@ class VmmModelHandle:
             raise
 
     def _host_pieces(self, block_idx: int) -> list[tuple[int, torch.Tensor]]:
-        if self._file is not None and block_idx < len(self._block_pieces):
-            view = self._file[2]
-            return [(dst, torch.frombuffer(view, dtype=torch.uint8, count=n, offset=off))
-                    for dst, off, n in self._block_pieces[block_idx] if n > 0]
+        if self._files and block_idx < len(self._block_pieces):
+            return [(dst, torch.frombuffer(self._files[path][2], dtype=torch.uint8, count=n, offset=off))
+                    for dst, path, off, n in self._block_pieces[block_idx] if n > 0]
         ram = self._ram_weight_refs[block_idx]
         if ram is not None:
             return [(0, ram.detach().reshape(-1).contiguous().view(torch.uint8))]
@@ -342,14 +356,12 @@ class VmmModelHandle:
             self.allocator.prefetch(self.slab_id, self.regions[block_idx])
         except Exception:
             pass
-        if self._file is not None and block_idx < len(self._block_pieces):
-            blk = self._block_pieces[block_idx]
-            if blk:
-                start = min(off for _d, off, _n in blk)
-                end = max(off + n for _d, off, n in blk)
+        if self._files and block_idx < len(self._block_pieces):
+            page = mmap.PAGESIZE
+            for _dst, path, off, n in self._block_pieces[block_idx]:
+                start = off // page * page
                 try:
-                    page = mmap.PAGESIZE
-                    self._file[1].madvise(mmap.MADV_WILLNEED, start // page * page, end - start // page * page)
+                    self._files[path][1].madvise(mmap.MADV_WILLNEED, start, off + n - start)
                 except (AttributeError, OSError, ValueError):
                     pass
 
@@ -373,9 +385,9 @@ class VmmModelHandle:
 
     def release_mmap(self) -> None:
         """Lets the OS drop the file's pages (they are re-read on the next fill)."""
-        if self._file is not None:
+        for _fh, mm, _view in self._files.values():
             try:
-                self._file[1].madvise(mmap.MADV_DONTNEED)
+                mm.madvise(mmap.MADV_DONTNEED)
             except (AttributeError, OSError):
                 pass
 
@@ -448,7 +460,7 @@ class VmmManager:
 
     def stats(self) -> dict:
         s = self.allocator.stats()
-        mm = sum(len(h._file[1]) for h in self.models.values() if h._file is not None)
+        mm = sum(len(f[1]) for h in self.models.values() for f in h._files.values())
         s["mmap_data_bytes"] = mm
         s["mmap_data_gb"] = round(mm / 1e9, 2)
         return s
