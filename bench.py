@@ -231,7 +231,7 @@ def write_dit_safetensors_sharded(model, directory: Path, seed: int) -> int:
     return total
 
 
-def _dit_config(kind: str, args, pinned: bool):
+def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
     import stagehand_amd as stagehand
 
     if kind == "squareq":
@@ -250,7 +250,7 @@ def _dit_config(kind: str, args, pinned: bool):
         cfg = stagehand.StagehandConfig(pinned_pool_mb=4096, pinned_slab_mb=256, vram_high_watermark_mb=19200,
                                         vram_low_watermark_mb=14400, prefetch_window_blocks=2,
                                         max_inflight_transfers=3, nan_inf_check=False, strict_bf16=False,
-                                        telemetry_enabled=True, pinned_source_cache=pinned)
+                                        telemetry_enabled=True, pinned_source_cache=pinned, file_reader=reader)
     cfg.telemetry_file = None
     return cfg
 
@@ -321,7 +321,7 @@ def timeline_stats(trace: dict, pcie_peak_gbps: float | None) -> dict:
     return res
 
 
-def _dit_run(kind: str, args, src: Path, layers, pinned: bool) -> dict:
+def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mmap") -> dict:
     import torch
 
     import stagehand_amd as stagehand
@@ -329,7 +329,7 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool) -> dict:
 
     model = _dit_model()  # a fresh module tree per runtime: conversion drops the module's weights
 
-    rt = stagehand.StagehandRuntime(model, _dit_config(kind, args, pinned), block_pattern=DIT_BLOCK_PATTERN,
+    rt = stagehand.StagehandRuntime(model, _dit_config(kind, args, pinned, reader), block_pattern=DIT_BLOCK_PATTERN,
                                     dtype=torch.bfloat16, inference_mode=True)
     if kind == "squareq":
         converted = rt.convert_registry_to_file_backed(str(src))
@@ -375,6 +375,7 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool) -> dict:
                 break
     res = {
         "source_mode": "pinned source images" if pinned else "bounded pinned pool (staged)",
+        "file_reader": reader if kind == "file" else None,
         "params_converted": converted,
         "int8_elements": sum(l.in_features * l.out_features for _n, l in dit_linear_layers(model)) if kind == "squareq" else None,
         "scale_rows": sum(l.out_features for _n, l in dit_linear_layers(model)) if kind == "squareq" else None,
@@ -602,7 +603,7 @@ def _vmm_run(args, src: Path) -> dict:
     from stagehand_amd.workloads import DIT_BLOCK_PATTERN
 
     model = _dit_model()
-    rt = stagehand.StagehandRuntime(model, _dit_config("file", args, False), block_pattern=DIT_BLOCK_PATTERN,
+    rt = stagehand.StagehandRuntime(model, _dit_config("file", args, False, args.file_reader), block_pattern=DIT_BLOCK_PATTERN,
                                     dtype=torch.bfloat16, inference_mode=True)
     rt.convert_registry_to_file_backed_sharded(str(src))
     handle = rt.vmm_register_model("dit", "bfloat16", str(src))
@@ -650,7 +651,8 @@ def _vmm_run(args, src: Path) -> dict:
         alloc.ensure_resident(handle.slab_id, handle.regions[0], stream).release()
     fast_us = (time.perf_counter() - t2) / n * 1e6
     st = rt.vmm.stats()
-    res = {"first_step_ms": round(first_ms, 1), "ms_per_step": round(ms, 2), "steps": args.dit_steps,
+    res = {"file_reader": args.file_reader, "first_step_ms": round(first_ms, 1), "ms_per_step": round(ms, 2),
+           "steps": args.dit_steps,
            "blocks_served_per_step": {k: v / args.dit_steps for k, v in served.items()},
            "mapped_gb": round(st["mapped_bytes"] / 1e9, 2), "vram_ceiling_gb": round(st["vram_ceiling"] / 1e9, 1),
            "granularity": st["granularity"], "maps": st["maps"], "evictions": st["evictions"],
@@ -661,6 +663,124 @@ def _vmm_run(args, src: Path) -> dict:
     gc.collect()
     torch.cuda.empty_cache()
     return res
+
+
+def _drop_page_cache(src: Path) -> int:
+    """Writes back and drops the shards' pages from the page cache (an unprivileged
+    cold start: POSIX_FADV_DONTNEED drops clean pages of the file). Returns the bytes."""
+    import gc
+
+    gc.collect()  # host views of an earlier runtime's mappings pin their pages
+    total = 0
+    for p in sorted(src.glob("*.safetensors")):
+        fd = os.open(p, os.O_RDONLY)
+        try:
+            os.fsync(fd)
+            os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+            total += os.fstat(fd).st_size
+        finally:
+            os.close(fd)
+    return total
+
+
+def _sample_read_gbps(src: Path, nbytes: int = 128 << 20) -> float:
+    """Read rate of the first ``nbytes`` of the last shard: tells a cold page cache (storage
+    rate) from a warm one (memory rate) after a drop."""
+    p = sorted(src.glob("*.safetensors"))[-1]
+    fd = os.open(p, os.O_RDONLY)
+    try:
+        t0 = time.perf_counter()
+        done = 0
+        while done < nbytes:
+            b = os.pread(fd, min(16 << 20, nbytes - done), done)
+            if not b:
+                break
+            done += len(b)
+        return done / (time.perf_counter() - t0) / 1e9
+    finally:
+        os.close(fd)
+
+
+def _first_steps(args, src: Path, reader: str, cold: bool, steps: int = 2, pinned: bool = False) -> dict:
+    """A fresh runtime on the config-3 shards; wall time of each of its first steps
+    (the first reads every block from the files; later ones keep part resident). With
+    ``pinned`` the first load of each block fills its pinned source image and later
+    loads DMA from the image."""
+    import gc
+
+    import torch
+
+    import stagehand_amd as stagehand
+    from stagehand_amd.workloads import DIT_BLOCK_PATTERN
+
+    model = _dit_model()
+    rt = stagehand.StagehandRuntime(model, _dit_config("file", args, pinned, reader), block_pattern=DIT_BLOCK_PATTERN,
+                                    dtype=torch.bfloat16, inference_mode=True)
+    rt.convert_registry_to_file_backed_sharded(str(src))
+    img, txt, vec = _dit_inputs(args.seed)
+    file_bytes = _drop_page_cache(src) if cold else sum(p.stat().st_size for p in src.glob("*.safetensors"))
+    sample = _sample_read_gbps(src)
+    torch.cuda.synchronize()
+    times, sent = [], []
+    for i in range(steps):
+        b0 = rt.engine.bytes_h2d
+        t0 = time.perf_counter()
+        rt.begin_step(i)
+        with torch.no_grad(), rt.managed_forward():
+            out = model(img, txt, vec)
+        rt.end_step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        sent.append(rt.engine.bytes_h2d - b0)
+    files = rt.scheduler._weight_files.files()
+    info = [f.info() for f in files]
+    res = {
+        "reader": reader,
+        "source": "pinned source images" if pinned else "bounded pinned pool (staged)",
+        "cache": "cold (dropped)" if cold else "page cache",
+        "sample_read_gbps_before": round(sample, 2),
+        "step_ms": [round(t * 1e3, 1) for t in times],
+        "first_step_file_gbps": round(file_bytes / times[0] / 1e9, 2),
+        "h2d_bytes_per_step": sent,
+        "bytes_direct": sum(i["bytes_direct"] for i in info) if info else None,
+        "bytes_buffered": sum(i["bytes_buffered"] for i in info) if info else None,
+        "bytes_cached": sum(i["bytes_cached"] for i in info) if info else None,
+        "bytes_bounced": sum(i["bytes_bounced"] for i in info) if info else None,
+        "out_finite": bool(torch.isfinite(out.float()).all()),
+    }
+    rt.shutdown()
+    for e in rt.registry.blocks_in_order():
+        rt.residency.get_entry(e.block_id).gpu_tensor = None
+    del rt, model, out, img, txt, vec
+    gc.collect()
+    torch.cuda.empty_cache()
+    return res
+
+
+def readers_leg(args, src: Path, main_reader: str) -> dict:
+    """The weight-file readers on the config-3 shards: the first two steps of a fresh
+    runtime from a cold page cache and from a warm one, and the steady-state step of
+    the readers other than the main leg's."""
+    import torch
+
+    out: dict = {"file_bytes": sum(p.stat().st_size for p in src.glob("*.safetensors"))}
+    for reader in ("mmap", "pread", "direct"):
+        log(f"dit/file: reader {reader}, cold first steps")
+        out[f"{reader}_cold"] = _first_steps(args, src, reader, cold=True)
+    log("dit/file: reader direct into pinned source images, cold first steps")
+    out["direct_pinned_cold"] = _first_steps(args, src, "direct", cold=True, steps=3, pinned=True)
+    for reader in ("mmap", "pread"):
+        log(f"dit/file: reader {reader}, warm first steps")
+        out[f"{reader}_warm"] = _first_steps(args, src, reader, cold=False)
+    for reader in ("mmap", "pread"):
+        if reader == main_reader:
+            continue
+        log(f"dit/file: reader {reader}, steady state")
+        r = _dit_run("file", args, src, None, False, reader)
+        out[f"{reader}_steady"] = {k: r[k] for k in ("ms_per_step", "streamed_gbps", "pcie_bytes_per_step",
+                                                     "peak_vram_gb", "timeline")}
+        torch.cuda.empty_cache()
+    return out
 
 
 def dit_leg(kind: str, args) -> dict:
@@ -693,10 +813,13 @@ def dit_leg(kind: str, args) -> dict:
                         "config3 bf16 Flux-style DiT (11.84 B params), sharded safetensors, 24 GB VRAM cap, prefetch window 2"),
            "source_write_s": round(setup_s, 1)}
     modes = {"staged": (False,), "pinned": (True,), "both": (False, True)}[args.dit_modes]
+    reader = args.file_reader if kind == "file" else "mmap"
     for pinned in modes:
-        log(f"dit/{kind}: streaming ({'pinned images' if pinned else 'staged'})")
-        res["pinned" if pinned else "staged"] = _dit_run(kind, args, src, layers, pinned)
+        log(f"dit/{kind}: streaming ({'pinned images' if pinned else 'staged'}, reader {reader})")
+        res["pinned" if pinned else "staged"] = _dit_run(kind, args, src, layers, pinned, reader)
         torch.cuda.empty_cache()
+    if kind == "file" and args.readers == "on":
+        res["readers"] = readers_leg(args, src, reader)
     best = min((res[m] for m in ("staged", "pinned") if m in res), key=lambda r: r["ms_per_step"])
     for k in ("ms_per_step", "streamed_gbps", "pcie_bytes_per_step", "block_bf16_bytes_per_step", "int8_elements",
               "scale_rows", "peak_vram_gb"):
@@ -768,6 +891,10 @@ def main() -> int:
     ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
     ap.add_argument("--train", default="on", choices=["on", "off"], help="config-5 streamed training step")
     ap.add_argument("--vmm", default="on", choices=["on", "off"], help="config-3 DiT served from the VMM backend")
+    ap.add_argument("--file-reader", default="pread", choices=["mmap", "pread", "direct"],
+                    help="weight-file reader of the config-3 leg")
+    ap.add_argument("--readers", default="on", choices=["on", "off"],
+                    help="config-3 shards through every file reader, cold and warm page cache")
     ap.add_argument("--train-steps", type=int, default=2)
     ap.add_argument("--train-warmup", type=int, default=1)
     args = ap.parse_args()

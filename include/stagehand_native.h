@@ -17,6 +17,7 @@
  *   SH_ERR_STATE     → RuntimeError        (reference: "No free GPU slots", turbo_src/engine.rs:189)
  *   SH_ERR_NOT_READY → not an error: the queried event/transfer is still pending
  *   SH_ERR_TIMEOUT   → TimeoutError
+ *   SH_ERR_IO        → OSError             (reference: open/mmap of a weight file, src/stagehand/scheduler.py:564-601)
  */
 #ifndef STAGEHAND_NATIVE_H
 #define STAGEHAND_NATIVE_H
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 1
+#define SH_ABI_VERSION 2
 
 enum sh_status {
   SH_OK = 0,
@@ -38,7 +39,8 @@ enum sh_status {
   SH_ERR_NOT_READY = 4,
   SH_ERR_STATE = 5,
   SH_ERR_TIMEOUT = 6,
-  SH_ERR_WATERMARK = 7
+  SH_ERR_WATERMARK = 7,
+  SH_ERR_IO = 8
 };
 
 /* Thread-local description of the last failure on the calling thread. */
@@ -214,6 +216,55 @@ int sh_pool_release(sh_pool* pool, uint32_t slab);
 int sh_pool_release_after(sh_pool* pool, uint32_t slab, void* stream);
 int sh_pool_get_stats(sh_pool* pool, sh_pool_stats* stats);
 
+/* ───────────────────────── weight files ─────────────────────────
+ * Bulk reads of weight files into host memory: the replacement of the
+ * per-parameter reads through an mmap (torch.frombuffer over the mapping, then
+ * copy_ into the slab) of src/stagehand/scheduler.py:184-241 and 564-601, and
+ * of the VMM backend's mmap fills with madvise(WILLNEED) read-ahead
+ * (src/stagehand/vmm_backend.py:283-291).
+ *
+ * A read is cut into pieces of at most 8 MiB at 8 MiB file offsets, spread
+ * over the host copy threads, which first copy what the page cache holds
+ * (preadv2 RWF_NOWAIT); the rest is then read from storage in file order by
+ * up to 4 threads, each reading one contiguous run front to back on a
+ * descriptor of its own (interleaved cold reads of one file defeat the
+ * kernel's read-ahead). A file opened with
+ * SH_FILE_DIRECT also holds an O_DIRECT descriptor and is read around the page
+ * cache: straight into the destination (the storage DMA writes it) where the
+ * destination is congruent to the file offset modulo SH_FILE_ALIGN and the
+ * kernel can pin it (the unaligned head and tail then go through the page
+ * cache), else through a per-thread aligned bounce buffer — the route of
+ * hipHostMalloc'd memory, which the kernel refuses to pin for a DMA. Where the
+ * file system refuses O_DIRECT, the file is read buffered only
+ * (sh_file_info.direct = 0). Reads past the end of the file (as sized when it
+ * was opened) are SH_ERR_INVALID; failed reads SH_ERR_IO. */
+#define SH_FILE_DIRECT 1
+#define SH_FILE_ALIGN 4096
+enum sh_file_advice { SH_FILE_WILLNEED = 1, SH_FILE_DONTNEED = 2 };
+typedef struct sh_file sh_file;
+typedef struct sh_file_info {
+  uint64_t size;
+  uint64_t direct;          /* 1 when an O_DIRECT descriptor is open */
+  uint64_t bytes_direct;    /* bytes read with O_DIRECT into the destination so far */
+  uint64_t bytes_bounced;   /* bytes read with O_DIRECT through the bounce buffer so far */
+  uint64_t bytes_buffered;  /* bytes read through the page cache so far */
+  uint64_t bytes_cached;    /* of those, bytes the page cache already held */
+  uint64_t reads;           /* pread calls so far */
+} sh_file_info;
+typedef struct sh_file_range {
+  sh_file* file;
+  uint64_t file_off;
+  uint64_t bytes;
+  uint64_t dst;  /* byte offset from the destination base */
+} sh_file_range;
+int sh_file_open(const char* path, int flags, sh_file** out);
+int sh_file_close(sh_file* f);
+int sh_file_get_info(sh_file* f, sh_file_info* info);
+/* posix_fadvise over [offset, offset + bytes) (bytes 0: to the end of the file). */
+int sh_file_advise(sh_file* f, uint64_t offset, uint64_t bytes, int advice);
+/* Reads every range to base + range.dst on up to `threads` copy threads. */
+int sh_file_read_batch(const sh_file_range* ranges, size_t n, void* base, int threads);
+
 /* Multi-threaded host memcpy of a batch of (dst, src, bytes) items, used to
  * gather a block's parameters into its pinned slab (the per-parameter host
  * copy_ loops of src/stagehand/scheduler.py:168-181, 203-241, 263-325). */
@@ -266,6 +317,14 @@ typedef struct sh_load_request {
    * not change. Before re-gathering into an image the loader waits for the
    * previous copy out of it. */
   void* image;
+  /* Optional file ranges (sh_file_range, dst = byte offset in the source like
+   * pieces[i].dst), read into the slab chunks (or the image) by the same copy
+   * threads, with pread / O_DIRECT (sh_file_open). The files must stay open
+   * until the ticket is issued. When the loader starts a ticket, it asks the
+   * kernel to read ahead (POSIX_FADV_WILLNEED) the buffered ranges of that
+   * ticket and of the ticket queued after it. */
+  const struct sh_file_range* ranges;
+  uint64_t n_ranges;
 } sh_load_request;
 
 typedef struct sh_loader sh_loader;

@@ -7,7 +7,8 @@ telling how to build it.
 Status codes map to the exception types the reference raises for the same
 conditions (turbo_src/lib.rs:38-40 → RuntimeError, turbo_src/lib.rs:59-61 →
 ValueError, src/stagehand/pool.py:133-139 → StagehandOOMError,
-vmm_src/error.rs:30-53 → MemoryError for watermark refusals).
+vmm_src/error.rs:30-53 → MemoryError for watermark refusals, and OSError for
+weight-file reads, as the reference's open/mmap of a weight file raises).
 """
 from __future__ import annotations
 
@@ -46,6 +47,12 @@ SH_ERR_NOT_READY = 4
 SH_ERR_STATE = 5
 SH_ERR_TIMEOUT = 6
 SH_ERR_WATERMARK = 7
+SH_ERR_IO = 8
+
+SH_FILE_DIRECT = 1
+SH_FILE_ALIGN = 4096
+SH_FILE_WILLNEED = 1
+SH_FILE_DONTNEED = 2
 
 KIND_I8_ROWSCALE_BF16 = 1
 KIND_I8_ROWSCALE_F32 = 2
@@ -135,6 +142,11 @@ _SIGNATURES: dict[str, list] = {
     "sh_pool_release_after": [_vp, _u32, _vp],
     "sh_pool_get_stats": [_vp, _vp],
     "sh_host_copy_batch": [_vp, _sz, _i32],
+    "sh_file_open": [ctypes.c_char_p, _i32, ctypes.POINTER(_vp)],
+    "sh_file_close": [_vp],
+    "sh_file_get_info": [_vp, _vp],
+    "sh_file_advise": [_vp, ctypes.c_uint64, ctypes.c_uint64, _i32],
+    "sh_file_read_batch": [_vp, _sz, _vp, _i32],
     "sh_loader_create": [_vp, _i32, ctypes.POINTER(_vp)],
     "sh_loader_destroy": [_vp],
     "sh_loader_streams": [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
@@ -190,7 +202,13 @@ LOAD_REQUEST_DTYPE = np.dtype([
     ("pieces", "<u8"), ("n_pieces", "<u8"), ("src_bytes", "<u8"), ("plan", "<u8"), ("staging", "<u8"),
     ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
     ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"), ("image", "<u8"),
+    ("ranges", "<u8"), ("n_ranges", "<u8"),
 ])
+
+# Mirrors of `struct sh_file_range` / `struct sh_file_info`.
+FILE_RANGE_DTYPE = np.dtype([("file", "<u8"), ("file_off", "<u8"), ("bytes", "<u8"), ("dst", "<u8")])
+FILE_INFO_DTYPE = np.dtype([("size", "<u8"), ("direct", "<u8"), ("bytes_direct", "<u8"), ("bytes_bounced", "<u8"),
+                            ("bytes_buffered", "<u8"), ("bytes_cached", "<u8"), ("reads", "<u8")])
 
 # Mirror of `struct sh_pool_stats`.
 POOL_STATS_DTYPE = np.dtype([
@@ -208,7 +226,7 @@ VMM_REGION_DTYPE = np.dtype([("state", "<u4"), ("refcount", "<u4"), ("offset", "
 # Mirror of `struct sh_copy_item`.
 COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -264,6 +282,8 @@ def check(status: int, what: str = "") -> int:
         raise MemoryError(msg)
     if status == SH_ERR_TIMEOUT:
         raise TimeoutError(msg)
+    if status == SH_ERR_IO:
+        raise OSError(msg)
     raise RuntimeError(msg)
 
 

@@ -7,7 +7,9 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <functional>
 #include <string>
+#include <vector>
 
 #include "stagehand_native.h"
 
@@ -26,6 +28,32 @@ void clear_error();
       return ::sh::fail(SH_ERR_HIP, "HIP error %d (%s) in %s", (int)sh_e_,       \
                         hipGetErrorString(sh_e_), #call);                         \
   } while (0)
+
+// Runs fn(i) for every i in [0, n) on up to `threads` of the shared host copy
+// threads (the calling thread included); returns when all calls are done.
+void parallel_for(size_t n, unsigned threads, const std::function<void(size_t)>& fn);
+
+// One unit of host staging work: a memcpy (file == nullptr) or a read of
+// `bytes` at `file_off` of `file` into dst.
+struct IoPiece {
+  uint8_t* dst;
+  const uint8_t* src;
+  sh_file* file;
+  uint64_t file_off;
+  uint64_t bytes;
+};
+// Appends a memcpy cut into pieces of at most 8 MiB.
+void append_copy(std::vector<IoPiece>& out, void* dst, const void* src, uint64_t bytes);
+// Appends a file read cut at 8 MiB file offsets (pieces stay aligned for O_DIRECT).
+void append_read(std::vector<IoPiece>& out, sh_file* f, uint64_t file_off, uint64_t bytes, void* dst);
+// Checks that [file_off, file_off + bytes) lies inside the file (SH_ERR_INVALID otherwise).
+int check_range(const sh_file* f, uint64_t file_off, uint64_t bytes, const char* who);
+// Executes the pieces on up to `threads` copy threads; SH_ERR_IO (with the
+// failing file, offset and errno in the last error) when a read fails.
+int run_io(const std::vector<IoPiece>& pieces, int threads);
+// The buffered descriptor of a file that has no O_DIRECT descriptor, else -1:
+// the descriptor on which read-ahead advice is worth giving.
+int advice_fd(const sh_file* f);
 
 // floor(n / d) for every 32-bit n, with magic = ceil(2^64 / d) for d >= 2 and
 // magic = 0 for d == 1. The quotient is floor(n * magic / 2^64): with

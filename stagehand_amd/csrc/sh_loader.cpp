@@ -16,15 +16,22 @@
 //                   destination buffer was allocated there), enqueue request.
 //   worker thread : acquire slab (blocks while every slab is busy; fenced
 //                   slabs come back as their H2D copies drain), gather the
-//                   pieces into the slab with the multi-threaded host copy,
+//                   pieces into the slab with the multi-threaded host copy
+//                   and read its file ranges (pread / O_DIRECT) on the same
+//                   threads,
 //                   copy stream: wait `ready`, H2D slab → staging (or → dst),
 //                   record `copied`; release the slab after `copied`;
 //                   unpack stream: wait `copied`, launch the plan, record `done`.
 //   caller thread : sh_loader_stream_wait(ticket, compute stream) makes the
 //                   compute stream wait for `done` without blocking the host.
 // The worker owns the host-side staging, so the Python hook thread never
-// copies weight bytes and never waits for a copy to finish.
+// copies weight bytes and never waits for a copy to finish. When it starts a
+// ticket, the buffered file ranges of that ticket and of the one queued behind
+// it go to an advisor thread that asks the kernel to read them ahead
+// (POSIX_FADV_WILLNEED): the whole range is queued as large reads at once, and
+// the next block is already being read while the current one is staged.
 
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -55,6 +62,8 @@ struct Ticket {
   std::string error;
   // request
   std::vector<sh_copy_item> pieces;
+  std::vector<sh_file_range> ranges;
+  bool advised = false;
   uint64_t src_bytes = 0;
   const sh_plan* plan = nullptr;
   void* staging = nullptr;
@@ -90,6 +99,16 @@ struct sh_loader {
   bool timing = false;  // copied/done/start are timing events
   std::vector<hipEvent_t> spare_timing_events;
   std::thread worker;
+  // read-ahead advice: (fd, offset, bytes) handed to the advisor thread
+  struct Advice {
+    int fd;
+    uint64_t off, bytes;
+  };
+  std::mutex advice_mu;
+  std::condition_variable advice_cv;
+  std::deque<Advice> advice;
+  bool advice_stop = false;
+  std::thread advisor;
 };
 
 extern "C" int sh_unpack(const sh_plan* plan, const void* src, size_t src_bytes, const float* scales,
@@ -142,20 +161,19 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord(start)");
   }
   if (t.image != nullptr) {
-    // Pinned source image: refresh the given pieces, then one DMA straight from it.
-    if (!t.pieces.empty()) {
+    // Pinned source image: refresh the given pieces and ranges, then one DMA straight from it.
+    if (!t.pieces.empty() || !t.ranges.empty()) {
       auto f = L->image_fence.find(t.image);
       if (f != L->image_fence.end()) {
         e = hipEventSynchronize(f->second);
         if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize(image fence)");
       }
-      std::vector<sh_copy_item> items(t.pieces.size());
-      for (size_t i = 0; i < t.pieces.size(); ++i) {
-        items[i].dst = (uint8_t*)t.image + (uintptr_t)t.pieces[i].dst;
-        items[i].src = t.pieces[i].src;
-        items[i].bytes = t.pieces[i].bytes;
-      }
-      int st = sh_host_copy_batch(items.data(), items.size(), t.copy_threads);
+      std::vector<sh::IoPiece> io;
+      for (const sh_copy_item& p : t.pieces)
+        sh::append_copy(io, (uint8_t*)t.image + (uintptr_t)p.dst, p.src, p.bytes);
+      for (const sh_file_range& r : t.ranges)
+        sh::append_read(io, r.file, r.file_off, r.bytes, (uint8_t*)t.image + r.dst);
+      int st = sh::run_io(io, t.copy_threads);
       if (st != SH_OK) {
         err = sh_last_error();
         return st;
@@ -177,8 +195,7 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
     e = hipEventRecord(fence, L->copy_stream);
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord(image fence)");
   }
-  std::vector<sh_copy_item> items;
-  items.reserve(t.pieces.size());
+  std::vector<sh::IoPiece> io;
   for (uint64_t c0 = 0; t.image == nullptr && c0 < t.src_bytes; c0 += L->slab_bytes) {
     const uint64_t c1 = std::min<uint64_t>(t.src_bytes, c0 + L->slab_bytes);
     uint32_t slab = 0;
@@ -190,18 +207,18 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
     }
     void* slab_ptr = nullptr;
     sh_pool_slab_ptr(L->pool, slab, &slab_ptr);
-    items.clear();
+    io.clear();
     for (const sh_copy_item& p : t.pieces) {
       const uint64_t p0 = (uint64_t)(uintptr_t)p.dst, p1 = p0 + p.bytes;
       const uint64_t a = std::max(p0, c0), b = std::min(p1, c1);
-      if (a >= b) continue;
-      sh_copy_item it;
-      it.dst = (uint8_t*)slab_ptr + (a - c0);
-      it.src = (const uint8_t*)p.src + (a - p0);
-      it.bytes = b - a;
-      items.push_back(it);
+      if (a < b) sh::append_copy(io, (uint8_t*)slab_ptr + (a - c0), (const uint8_t*)p.src + (a - p0), b - a);
     }
-    st = sh_host_copy_batch(items.data(), items.size(), t.copy_threads);
+    for (const sh_file_range& r : t.ranges) {
+      const uint64_t r0 = r.dst, r1 = r0 + r.bytes;
+      const uint64_t a = std::max(r0, c0), b = std::min(r1, c1);
+      if (a < b) sh::append_read(io, r.file, r.file_off + (a - r0), b - a, (uint8_t*)slab_ptr + (a - c0));
+    }
+    st = sh::run_io(io, t.copy_threads);
     if (st != SH_OK) {
       err = sh_last_error();
       sh_pool_release(L->pool, slab);
@@ -242,6 +259,21 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   return SH_OK;
 }
 
+// Queues POSIX_FADV_WILLNEED for the buffered file ranges of `t` (once per
+// ticket). One advice call per range makes the kernel queue the whole range's
+// reads at once, in large requests, where the copy threads' preads alone would
+// read a cold file one small read-ahead window at a time. Called with L->mu held.
+void advise(sh_loader* L, Ticket& t) {
+  if (t.advised || t.ranges.empty()) return;
+  t.advised = true;
+  std::lock_guard<std::mutex> ag(L->advice_mu);
+  for (const sh_file_range& r : t.ranges) {
+    const int fd = sh::advice_fd(r.file);
+    if (fd >= 0 && r.bytes > 0) L->advice.push_back({fd, r.file_off, r.bytes});
+  }
+  L->advice_cv.notify_one();
+}
+
 void worker_loop(sh_loader* L) {
   for (;;) {
     uint64_t id = 0;
@@ -253,6 +285,10 @@ void worker_loop(sh_loader* L) {
       id = L->queue.front();
       L->queue.pop_front();
       t = &L->tickets.at(id);  // unordered_map references stay valid across inserts
+      // read-ahead advice for this ticket's files, then the next one's (their files are
+      // open until the tickets are issued: take the descriptors now)
+      advise(L, *t);
+      if (!L->queue.empty()) advise(L, L->tickets.at(L->queue.front()));
     }
     std::string err;
     const int st = run_request(L, *t, err);
@@ -263,8 +299,28 @@ void worker_loop(sh_loader* L) {
       t->state = st == SH_OK ? TicketState::Issued : TicketState::Failed;
       t->pieces.clear();
       t->pieces.shrink_to_fit();
+      t->ranges.clear();
+      t->ranges.shrink_to_fit();
     }
     L->issued_cv.notify_all();
+  }
+}
+
+// Gives read-ahead advice off the worker thread: posix_fadvise(WILLNEED) starts
+// the reads but may block while it queues them. The descriptors were taken
+// while their files were known to be open; advice on a descriptor that has
+// since been closed or reused is at worst a wasted hint.
+void advisor_loop(sh_loader* L) {
+  for (;;) {
+    sh_loader::Advice a;
+    {
+      std::unique_lock<std::mutex> lk(L->advice_mu);
+      L->advice_cv.wait(lk, [&] { return L->advice_stop || !L->advice.empty(); });
+      if (L->advice_stop) return;
+      a = L->advice.front();
+      L->advice.pop_front();
+    }
+    (void)::posix_fadvise(a.fd, (off_t)a.off, (off_t)a.bytes, POSIX_FADV_WILLNEED);
   }
 }
 
@@ -307,6 +363,7 @@ extern "C" int sh_loader_create(sh_pool* pool, int copy_threads, sh_loader** out
     return sh::fail(SH_ERR_HIP, "sh_loader_create: HIP error %d (%s)", (int)e, hipGetErrorString(e));
   }
   L->worker = std::thread(worker_loop, L);
+  L->advisor = std::thread(advisor_loop, L);
   *out = L;
   return SH_OK;
 }
@@ -320,6 +377,12 @@ extern "C" int sh_loader_destroy(sh_loader* L) {
   }
   L->cv.notify_all();
   if (L->worker.joinable()) L->worker.join();
+  {
+    std::lock_guard<std::mutex> ag(L->advice_mu);
+    L->advice_stop = true;
+  }
+  L->advice_cv.notify_all();
+  if (L->advisor.joinable()) L->advisor.join();
   (void)hipStreamSynchronize(L->copy_stream);
   (void)hipStreamSynchronize(L->unpack_stream);
   for (auto& kv : L->tickets) give_events(L, kv.second);
@@ -351,6 +414,14 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
     const uint64_t end = (uint64_t)(uintptr_t)p.dst + p.bytes;
     if (end < p.bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: piece %llu overflows", (unsigned long long)i);
     if (p.bytes > 0 && p.src == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: piece %llu has no source", (unsigned long long)i);
+    need = need > end ? need : end;
+  }
+  if (req->n_ranges > 0 && req->ranges == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: ranges is NULL");
+  for (uint64_t i = 0; i < req->n_ranges; ++i) {
+    const sh_file_range& r = req->ranges[i];
+    if (int st = sh::check_range(r.file, r.file_off, r.bytes, "sh_loader_submit")) return st;
+    const uint64_t end = r.dst + r.bytes;
+    if (end < r.bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: range %llu overflows", (unsigned long long)i);
     need = need > end ? need : end;
   }
   if (need > req->src_bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: pieces end at %llu, past src_bytes %llu",
@@ -391,6 +462,7 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
     return sh::fail(SH_ERR_HIP, "sh_loader_submit: HIP error %d (%s)", (int)e, hipGetErrorString(e));
   }
   t.pieces.assign(req->pieces, req->pieces + req->n_pieces);
+  if (req->n_ranges > 0) t.ranges.assign(req->ranges, req->ranges + req->n_ranges);
   t.src_bytes = req->src_bytes;
   t.plan = req->plan;
   t.staging = req->staging;

@@ -323,6 +323,10 @@ constexpr size_t kCopyPiece = 8u << 20;  // 8 MiB pieces spread over the workers
 
 }  // namespace
 
+void sh::parallel_for(size_t n, unsigned threads, const std::function<void(size_t)>& fn) {
+  CopyPool::get().parallel_for(n, threads, fn);
+}
+
 extern "C" int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threads) {
   sh::clear_error();
   if (n > 0 && items == nullptr) return sh::fail(SH_ERR_INVALID, "sh_host_copy_batch: items is NULL");

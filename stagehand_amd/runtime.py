@@ -95,7 +95,8 @@ class StagehandRuntime:
 
             if _vmm_mod.is_available():
                 try:
-                    self._vmm = _vmm_mod.VmmManager(device=torch.cuda.current_device(), engine=self._engine)
+                    self._vmm = _vmm_mod.VmmManager(device=torch.cuda.current_device(), engine=self._engine,
+                                                    file_reader=getattr(config, "file_reader", "mmap"))
                     for i, entry in enumerate(self._registry.blocks_in_order()):
                         self._vmm_block_id_to_idx[entry.block_id] = i
                 except Exception as e:  # noqa: BLE001 — the block-swap path still works

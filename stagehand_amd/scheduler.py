@@ -36,6 +36,7 @@ from typing import TYPE_CHECKING, Any, Protocol
 import torch
 from torch import nn
 
+from stagehand_amd.fileio import FileCache, FileRange
 from stagehand_amd.residency import BlockState
 from stagehand_amd.staging import PlanCache, SourceBuilder, squareq_weight_tensors
 from stagehand_amd.transfer import NativeEvent
@@ -134,6 +135,20 @@ def _detach_params(module: nn.Module, layout: Layout) -> None:
         _set_param_data(module, name, torch.empty(0, dtype=dtype))
 
 
+def _runtime_dtype_on_host(value: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """A module-resident parameter of a file- or SquareQ-backed block, in the runtime dtype.
+
+    Eviction saves such parameters back in the runtime dtype, so a parameter that
+    starts out in another dtype (fp32 norm weights of a bf16 model) changes dtype
+    after the block's first eviction. Casting it on the host at every load keeps
+    the block's source layout, and so its pinned source image, the same from the
+    first load on. The values are those of the device cast: torch's CPU
+    conversion rounds to nearest even, as the unpack kernel does."""
+    if value.dtype == dtype or not value.is_floating_point():
+        return value
+    return value.detach().to(device="cpu", dtype=dtype)
+
+
 def _flatten_params_into_buffer(module: nn.Module, buffer: torch.Tensor, layout: Layout) -> None:
     """Host path (no GPU): ``region.copy_(param.to(dtype))`` per parameter (src/stagehand/scheduler.py:168-181)."""
     params = dict(module.named_parameters())
@@ -185,6 +200,12 @@ class StagehandScheduler:
         self._eriquant_adapter = None
         self._file_maps: dict[str, tuple[Any, mmap.mmap, memoryview]] = {}
         self._file_tensor_views: dict[tuple, torch.Tensor] = {}
+        reader = getattr(config, "file_reader", "mmap")
+        if reader not in ("mmap", "pread", "direct"):
+            raise ValueError(f"file_reader must be 'mmap', 'pread' or 'direct', got {reader!r}")
+        # native weight-file reads (file_reader "pread"/"direct"): the device path only
+        self._file_reader = reader if self._has_cuda else "mmap"
+        self._weight_files = FileCache()
         self._squareq_layers: dict[str, dict[str, Any]] = {}
         self._module_param_caches: dict[str, dict[str, torch.Tensor]] = {}
         self._plans = PlanCache()
@@ -361,6 +382,7 @@ class StagehandScheduler:
                 except Exception:
                     pass
         self._file_maps.clear()
+        self._weight_files.close()
         self._squareq_layers.clear()
         self._module_param_caches.clear()
         self._plans.clear()
@@ -605,16 +627,23 @@ class StagehandScheduler:
         specs = {s.param_name: s for s in block_entry.file_param_specs}
         mutable = set(block_entry.module_param_names)
         sharded = block_entry.source_format == "safetensors_sharded"
-        base_view = None if sharded else self._get_file_view(str(block_entry.source_path))
+        native = self._file_reader != "mmap"
         for name, _shape, dtype, offset, numel in layout:
             spec = specs.get(name)
             if spec is not None:
                 path = spec.file_path if (spec.file_path and sharded) else str(block_entry.source_path)
-                view = self._get_file_view(path) if (spec.file_path and sharded) else base_view
+                if native:
+                    wf = self._weight_files.get(str(Path(path).expanduser()), self._file_reader == "direct")
+                    fr = FileRange(wf, int(spec.file_offset), int(spec.source_nbytes))
+                    if b.add_file_param(offset, fr, spec.source_dtype,
+                                        int(spec.source_nbytes) // spec.source_dtype.itemsize):
+                        continue
+                view = self._get_file_view(path) if (spec.file_path and sharded) else self._get_file_view(
+                    str(block_entry.source_path))
                 b.add_param(offset, self._get_file_tensor_view(path, spec, view))
                 continue
             if name in mutable and name in params and params[name].data.numel() == numel:
-                b.add_param(offset, params[name].data, mutable=True)
+                b.add_param(offset, _runtime_dtype_on_host(params[name].data, dtype), mutable=True)
                 continue
             b.add_zero(offset, numel * dtype.itemsize)
 
@@ -679,7 +708,7 @@ class StagehandScheduler:
             if name in mutable and name in params:
                 value = self._module_value(block_entry.block_id, params, name, numel, cache)
                 if value is not None:
-                    b.add_param(offset, value, mutable=True)
+                    b.add_param(offset, _runtime_dtype_on_host(value, dtype), mutable=True)
                     continue
             b.add_zero(offset, nbytes)
 

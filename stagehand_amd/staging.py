@@ -12,7 +12,10 @@ raw source pieces plus an unpack plan:
   format) plus per-row fp32 scales (and zero points when any is non-zero) and
   become SH_KIND_I8_ROWSCALE_* regions, dequantised on the device — half the
   PCIe bytes of a bf16 block;
-* missing parameters become zero-fill regions.
+* missing parameters become zero-fill regions;
+* parameters read from a weight file by the native reader are
+  :class:`~stagehand_amd.fileio.FileRange` pieces; in a plan layout they are
+  placed in file order and neighbours in the file merge into one read.
 
 When every region is a byte copy or zero fill, the slab image equals the
 destination image and no kernel runs (``plan is None``: a single H2D copy).
@@ -28,6 +31,7 @@ from typing import Any, Mapping
 import numpy as np
 import torch
 
+from stagehand_amd.fileio import FileRange
 from stagehand_amd.transfer import BlockSource
 from stagehand_amd.unpack import (
     KIND_BF16_F32,
@@ -105,6 +109,25 @@ class SourceBuilder:
             self._mutable.pop()
             raise ValueError(f"no device conversion from {v.dtype} to {rt}")
 
+    def add_file_param(self, dst_off: int, frange: FileRange, source_dtype: torch.dtype, numel: int) -> bool:
+        """``dst ← file bytes.to(runtime_dtype)`` for a tensor stored contiguously in a weight file.
+        Returns False (nothing added) for a source dtype the device cannot convert from raw
+        bytes; the caller then reads that tensor through a host view."""
+        rt = self.runtime_dtype
+        if source_dtype == rt:
+            kind, cols = KIND_COPY_BYTES, numel * rt.itemsize
+        elif rt == torch.bfloat16 and source_dtype == torch.float32:
+            kind, cols = KIND_F32_BF16, numel
+        elif rt == torch.float32 and source_dtype == torch.bfloat16:
+            kind, cols = KIND_BF16_F32, numel
+        else:
+            return False
+        if frange.nbytes != numel * source_dtype.itemsize:
+            raise ValueError(f"file range of {frange.nbytes} bytes does not hold {numel} {source_dtype} values")
+        self._regions.append((kind, dst_off, frange, 1, cols, 0, 0))
+        self._mutable.append(False)
+        return True
+
     def add_zero(self, dst_off: int, nbytes: int) -> None:
         if nbytes > 0:
             self._regions.append((KIND_ZERO_BYTES, dst_off, None, 1, nbytes, 0, 0))
@@ -141,20 +164,37 @@ class SourceBuilder:
             key = repr([(o, t.numel()) for o, t in pieces]).encode() + b"|direct|" + str(self.dst_bytes).encode()
             return BlockSource(pieces=pieces, src_bytes=self.dst_bytes, key=key, mutable=frozenset(mutable)), None
 
-        pieces: list[tuple[int, torch.Tensor]] = []
+        pieces: list[tuple[int, Any]] = []
         mutable = set()
         rows: list[tuple] = []
         cursor = 0
         scale_row = 0
-        for (kind, dst_off, t, r, c, ld, srows), mut in zip(self._regions, self._mutable):
+        # file ranges go first, in file order, so that neighbours in the file are
+        # neighbours in the slab (one read each run); the rest keep their order
+        order = sorted(range(len(self._regions)), key=lambda i: (
+            0, self._regions[i][2].file.path, self._regions[i][2].offset) if isinstance(self._regions[i][2], FileRange)
+            else (1, "", i))
+        for i in order:
+            (kind, dst_off, t, r, c, ld, srows), mut = self._regions[i], self._mutable[i]
             if kind == KIND_ZERO_BYTES:
                 rows.append((kind, 0, dst_off, r, c, 0, 0))
                 continue
-            off = _align(cursor)
-            if mut:
-                mutable.add(len(pieces))
-            pieces.append((off, t))
-            cursor = off + t.numel()
+            if isinstance(t, FileRange):
+                prev = pieces[-1] if pieces else None
+                if (prev is not None and isinstance(prev[1], FileRange) and prev[1].file is t.file
+                        and prev[1].offset + prev[1].nbytes == t.offset):
+                    off = cursor  # continues the previous range in the file: one read
+                    pieces[-1] = (prev[0], FileRange(t.file, prev[1].offset, prev[1].nbytes + t.nbytes))
+                else:
+                    off = _align(cursor)
+                    pieces.append((off, t))
+                cursor = off + t.nbytes
+            else:
+                off = _align(cursor)
+                if mut:
+                    mutable.add(len(pieces))
+                pieces.append((off, t))
+                cursor = off + t.numel()
             rows.append((kind, off, dst_off, r, c, ld, scale_row))
             scale_row += srows
         scale_off = zp_off = -1

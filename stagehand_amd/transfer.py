@@ -33,7 +33,7 @@ import numpy as np
 import torch
 
 from stagehand_amd import _native
-from stagehand_amd._native import COPY_ITEM_DTYPE, LOAD_REQUEST_DTYPE
+from stagehand_amd._native import COPY_ITEM_DTYPE, FILE_RANGE_DTYPE, LOAD_REQUEST_DTYPE
 from stagehand_amd.errors import TransferError
 
 if TYPE_CHECKING:
@@ -95,10 +95,11 @@ class TransferHandle:
 
 @dataclass
 class BlockSource:
-    """What one block load sends: slab pieces (offset, host tensor), the bytes
-    to send, and optionally an unpack plan with the offsets of its scales."""
+    """What one block load sends: slab pieces (offset, host tensor or
+    :class:`~stagehand_amd.fileio.FileRange`), the bytes to send, and optionally
+    an unpack plan with the offsets of its scales."""
 
-    pieces: list[tuple[int, torch.Tensor]]
+    pieces: list[tuple[int, Any]]
     src_bytes: int
     plan: "UnpackPlan | None" = None
     scale_off: int = -1
@@ -270,14 +271,21 @@ class AsyncTransferEngine:
             image, fresh = self._image_for(block_id, source)
             if not fresh:
                 pieces = [p for i, p in enumerate(source.pieces) if i in source.mutable]
-        items = np.zeros(len(pieces), dtype=COPY_ITEM_DTYPE)
+        tensors = [(off, t) for off, t in pieces if isinstance(t, torch.Tensor)]
+        files = [(off, t) for off, t in pieces if not isinstance(t, torch.Tensor)]
+        items = np.zeros(len(tensors), dtype=COPY_ITEM_DTYPE)
         keep: list = [gpu_dest]
-        for i, (off, t) in enumerate(pieces):
+        for i, (off, t) in enumerate(tensors):
             if t.device.type != "cpu" or not t.is_contiguous():
                 raise ValueError(f"block {block_id}: piece {i} must be a contiguous host tensor")
             items[i] = (off, t.data_ptr(), t.numel() * t.element_size())
             keep.append(t)
         keep.append(items)
+        ranges = np.zeros(len(files), dtype=FILE_RANGE_DTYPE)
+        for i, (off, fr) in enumerate(files):
+            ranges[i] = (fr.file.handle, fr.offset, fr.nbytes, off)
+            keep.append(fr.file)
+        keep.append(ranges)
         req = np.zeros(1, dtype=LOAD_REQUEST_DTYPE)
         req[0]["pieces"] = items.ctypes.data
         req[0]["n_pieces"] = len(items)
@@ -289,6 +297,8 @@ class AsyncTransferEngine:
         req[0]["n_scale"] = source.n_scale
         req[0]["copy_threads"] = self._copy_threads
         req[0]["image"] = image
+        req[0]["ranges"] = ranges.ctypes.data if len(ranges) else 0
+        req[0]["n_ranges"] = len(ranges)
         if source.plan is not None:
             if dest_on_loader_stream:
                 with torch.cuda.stream(self._loader_copy_stream()):

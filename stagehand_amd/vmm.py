@@ -27,7 +27,7 @@ import ctypes
 import logging
 import mmap
 from pathlib import Path
-from typing import Optional
+from typing import Any, Optional
 
 import numpy as np
 import torch
@@ -220,8 +220,13 @@ class VmmModelHandle:
     """One slab per model, one region per block (vmm_backend.py:86-359)."""
 
     def __init__(self, allocator: SlabAllocator, model_id: str, block_sizes: list[int], dtype: str,
-                 engine=None) -> None:
+                 engine=None, file_reader: str = "mmap") -> None:
+        if file_reader not in ("mmap", "pread", "direct"):
+            raise ValueError(f"file_reader must be 'mmap', 'pread' or 'direct', got {file_reader!r}")
         self.allocator = allocator
+        # "pread"/"direct": fills read the weight files with the native reader (file ranges
+        # in the block load) instead of through mappings; needs the block loader
+        self._file_reader = file_reader if engine is not None else "mmap"
         self.model_id = model_id
         self.dtype = dtype
         self.block_count = len(block_sizes)
@@ -242,6 +247,7 @@ class VmmModelHandle:
         self._current_priority = 0
         self._destroyed = False
         self._files: dict[str, tuple] = {}  # path → (file object, mmap, memoryview)
+        self._weight_files: dict[str, "WeightFile"] = {}  # path → native reader (file_reader != "mmap")
         self._block_pieces: list[list[tuple[int, str, int, int]]] = []  # per block: (dst off, file, file off, bytes)
         self._ram_weight_refs: list[torch.Tensor | None] = [None] * self.block_count
 
@@ -282,6 +288,11 @@ class VmmModelHandle:
             pieces.append(blk)
         self._close_file()
         for path in dict.fromkeys(p for blk in pieces for _d, p, _o, _n in blk):
+            if self._file_reader != "mmap":
+                from stagehand_amd.fileio import WeightFile
+
+                self._weight_files[path] = WeightFile(path, direct=self._file_reader == "direct")
+                continue
             fh = open(path, "rb")
             mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
             self._files[path] = (fh, mm, memoryview(mm))
@@ -299,6 +310,11 @@ class VmmModelHandle:
                 except Exception:
                     pass
         self._files = {}
+        if self._weight_files and self._engine is not None:
+            self._engine.drain()  # queued loads may still read the files
+        for wf in self._weight_files.values():
+            wf.close()
+        self._weight_files = {}
 
     # ── block access ─────────────────────────────────────────────────
 
@@ -325,7 +341,12 @@ class VmmModelHandle:
                 handle.release()
             raise
 
-    def _host_pieces(self, block_idx: int) -> list[tuple[int, torch.Tensor]]:
+    def _host_pieces(self, block_idx: int) -> list[tuple[int, Any]]:
+        if self._weight_files and block_idx < len(self._block_pieces):
+            from stagehand_amd.fileio import FileRange
+
+            return [(dst, FileRange(self._weight_files[path], off, n))
+                    for dst, path, off, n in self._block_pieces[block_idx] if n > 0]
         if self._files and block_idx < len(self._block_pieces):
             return [(dst, torch.frombuffer(self._files[path][2], dtype=torch.uint8, count=n, offset=off))
                     for dst, path, off, n in self._block_pieces[block_idx] if n > 0]
@@ -356,6 +377,12 @@ class VmmModelHandle:
             self.allocator.prefetch(self.slab_id, self.regions[block_idx])
         except Exception:
             pass
+        if self._weight_files and block_idx < len(self._block_pieces):
+            for _dst, path, off, n in self._block_pieces[block_idx]:
+                try:
+                    self._weight_files[path].advise_willneed(off, n)
+                except OSError:
+                    pass
         if self._files and block_idx < len(self._block_pieces):
             page = mmap.PAGESIZE
             for _dst, path, off, n in self._block_pieces[block_idx]:
@@ -422,13 +449,15 @@ class VmmModelHandle:
 class VmmManager:
     """The allocator and its per-model handles (vmm_backend.py:365-440)."""
 
-    def __init__(self, device: int = 0, ceiling_mb: Optional[int] = None, engine=None) -> None:
+    def __init__(self, device: int = 0, ceiling_mb: Optional[int] = None, engine=None,
+                 file_reader: str = "mmap") -> None:
         if not is_available():
             raise RuntimeError("VMM backend not available")
         self.allocator = SlabAllocator(device=device, ceiling_mb=ceiling_mb)
         self.models: dict[str, VmmModelHandle] = {}
         self._priority_counter = 0
         self._engine = engine
+        self._file_reader = file_reader
         s = self.allocator.stats()
         log.info("VMM: allocator ready. ceiling=%.2fGB, granularity=%.1fMB", s["vram_ceiling"] / 1e9,
                  s["granularity"] / 1e6)
@@ -437,7 +466,8 @@ class VmmManager:
         if model_id in self.models:
             log.warning("VMM: %s already registered, replacing", model_id)
             self.models[model_id].destroy()
-        handle = VmmModelHandle(self.allocator, model_id, block_sizes, dtype, engine=self._engine)
+        handle = VmmModelHandle(self.allocator, model_id, block_sizes, dtype, engine=self._engine,
+                                file_reader=self._file_reader)
         self.models[model_id] = handle
         return handle
 

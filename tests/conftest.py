@@ -37,3 +37,18 @@ def pytest_collection_modifyitems(config: pytest.Config, items: list[pytest.Item
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(autouse=True)
+def _collect_earlier_runtimes(request: pytest.FixtureRequest):
+    """GPU tests set VRAM watermarks relative to torch.cuda.memory_allocated() at their
+    start: collect the device buffers an earlier test's runtime still holds in reference
+    cycles first, so they are not freed in the middle of the next test."""
+    if "gpu" in request.keywords and _has_gpu():
+        import gc
+
+        import torch
+
+        gc.collect()
+        torch.cuda.synchronize()
+    yield

@@ -213,13 +213,15 @@ def test_tensors_release_and_compute():
 
 
 @gpu
+@pytest.mark.parametrize("reader", ["pread", "mmap"])
 @pytest.mark.parametrize("mode", ["roomy", "tight", "tight_reopen"])
-def test_runtime_serves_blocks_from_vmm(tmp_path, mode):
+def test_runtime_serves_blocks_from_vmm(tmp_path, mode, reader):
     """A file-backed model registered with the VMM backend gives the unstreamed outputs.
     With a ceiling of two blocks the first eviction lowers the model slab's watermark and
     later blocks take the block-swap path (the parameters it holds in the module, such as
     the norms, must survive the VMM blocks); re-activating the model every step re-opens
-    the slab, so blocks are evicted, re-mapped and re-filled from the file."""
+    the slab, so blocks are evicted, re-mapped and re-filled from the file — by the native
+    reader or through mappings."""
     tight = mode != "roomy"
     import stagehand_amd as stagehand
     from tests.streaming_models import TinyStack, init_, save_safetensors
@@ -231,7 +233,7 @@ def test_runtime_serves_blocks_from_vmm(tmp_path, mode):
     model.requires_grad_(False)
     cfg = stagehand.StagehandConfig(pinned_pool_mb=64, pinned_slab_mb=4, vram_high_watermark_mb=200000,
                                     vram_low_watermark_mb=100000, prefetch_window_blocks=2, nan_inf_check=False,
-                                    strict_bf16=False, telemetry_enabled=False)
+                                    strict_bf16=False, telemetry_enabled=False, file_reader=reader)
     cfg.telemetry_file = None
     rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
                                     inference_mode=True)
@@ -262,4 +264,8 @@ def test_runtime_serves_blocks_from_vmm(tmp_path, mode):
         assert max(g for g in handle._filled_generation if g is not None) >= 2
     assert stats["unmap_failures"] == 0
     assert not rt._vmm_active_blocks
+    if reader == "pread":
+        read = sum(f.info()["bytes_buffered"] for f in handle._weight_files.values())
+        filled = sum(size for size, g in zip(handle.block_sizes, handle._filled_generation) if g is not None)
+        assert read >= filled > 0  # the blocks served from the VMM were filled by the native reader
     rt.shutdown()
