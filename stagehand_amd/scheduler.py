@@ -206,6 +206,8 @@ class StagehandScheduler:
         # native weight-file reads (file_reader "pread"/"direct"): the device path only
         self._file_reader = reader if self._has_cuda else "mmap"
         self._weight_files = FileCache()
+        self._v2_locations: dict[str, dict] = {}  # SquareQ V2 file → layer → tensor locations
+        self._v2_zp_nonzero: dict[tuple, bool] = {}
         self._squareq_layers: dict[str, dict[str, Any]] = {}
         self._module_param_caches: dict[str, dict[str, torch.Tensor]] = {}
         self._plans = PlanCache()
@@ -383,6 +385,7 @@ class StagehandScheduler:
                     pass
         self._file_maps.clear()
         self._weight_files.close()
+        self._v2_locations.clear()
         self._squareq_layers.clear()
         self._module_param_caches.clear()
         self._plans.clear()
@@ -668,16 +671,24 @@ class StagehandScheduler:
         params = dict(module.named_parameters())
         specs = {s.param_name: s for s in block_entry.squareq_param_specs}
         mutable = set(block_entry.module_param_names)
-        if block_entry.source_format == "squareq_v2":
-            layers = self._get_squareq_v2_layers(str(block_entry.source_path))
-        else:
-            layers = self._get_squareq_layers(str(block_entry.source_path))
+        path = str(block_entry.source_path)
+        v2 = block_entry.source_format == "squareq_v2"
+        native = v2 and self._file_reader != "mmap"
+        loaded: list[dict] = []
+
+        def layers() -> dict[str, Any]:  # host views, only when a region needs them
+            if not loaded:
+                loaded.append(self._get_squareq_v2_layers(path) if v2 else self._get_squareq_layers(path))
+            return loaded[0]
+
         cache = self._module_param_caches.setdefault(block_entry.block_id, {})
         for name, shape, dtype, offset, numel in layout:
             nbytes = numel * dtype.itemsize
             spec = specs.get(name)
+            if spec is not None and native and self._add_v2_file_region(b, path, spec, shape, numel, offset):
+                continue
             if spec is not None:
-                layer = layers.get(spec.layer_name)
+                layer = layers().get(spec.layer_name)
                 if isinstance(layer, dict):
                     if spec.kind == "weight":
                         tensors = squareq_weight_tensors(layer)
@@ -711,6 +722,63 @@ class StagehandScheduler:
                     b.add_param(offset, _runtime_dtype_on_host(value, dtype), mutable=True)
                     continue
             b.add_zero(offset, nbytes)
+
+    def _add_v2_file_region(self, b: SourceBuilder, path: str, spec, shape, numel: int, offset: int) -> bool:
+        """A SquareQ V2 weight or bias read by the native reader: the int8 rows, scales and zero
+        points are file ranges in the block source, with the branch structure of
+        src/stagehand/scheduler.py:285-308. Returns False where the tensor path must run
+        instead (no such layer, or a dtype that needs host work: non-int8 rows, non-fp32
+        scales or zero points, fp16 biases)."""
+        from stagehand_amd.squareq_v2 import read_v2_locations
+
+        key = str(Path(path).expanduser())
+        locs = self._v2_locations.get(key)
+        if locs is None:
+            locs = self._v2_locations[key] = read_v2_locations(key, str(Path(key).with_suffix(".manifest.json")))
+        loc = locs.get(spec.layer_name)
+        if loc is None:
+            return False
+        wf = self._weight_files.get(key, self._file_reader == "direct")
+        nbytes = numel * b.runtime_dtype.itemsize
+        if spec.kind == "bias":
+            if "bias" not in loc:
+                b.add_zero(offset, nbytes)
+                return True
+            off, nb, dt, _shape = loc["bias"]
+            return b.add_file_param(offset, FileRange(wf, off, nb), dt, nb // dt.itemsize)
+        if spec.kind != "weight" or "qweight" not in loc or "scale" not in loc:
+            return False
+        q_off, q_nb, q_dt, q_shape = loc["qweight"]
+        s_off, s_nb, s_dt, _ = loc["scale"]
+        z = loc.get("zero_point")
+        if q_dt != torch.int8 or len(q_shape) == 0 or s_dt != torch.float32 or (z is not None and z[2] != torch.float32):
+            return False
+        out_dim = int(shape[0]) if len(shape) else 0
+        in_flat = numel // max(out_dim, 1) if out_dim else 0
+        if len(shape) == 0 or out_dim <= 0 or in_flat <= 0:
+            b.add_zero(offset, nbytes)
+            return True
+        rows_q = int(q_shape[0])
+        ld = q_nb // rows_q if rows_q > 0 else 0
+        s_n = s_nb // 4
+        z_n = z[1] // 4 if z is not None else s_n  # a missing zero point is zeros like the scales
+        if min(s_n, out_dim) != out_dim or min(z_n, out_dim) != out_dim:
+            b.add_zero(offset, nbytes)
+            return True
+        if rows_q < out_dim or ld < in_flat:
+            raise ValueError(f"SquareQ layer {spec.layer_name!r}: qweight {tuple(q_shape)} is smaller than "
+                             f"{out_dim}x{in_flat}")
+        zp = None
+        if z is not None:
+            zkey = (key, spec.layer_name, out_dim)
+            nonzero = self._v2_zp_nonzero.get(zkey)
+            if nonzero is None:
+                vals = wf.read_into(torch.empty(out_dim, dtype=torch.float32), z[0], 4 * out_dim)
+                nonzero = self._v2_zp_nonzero[zkey] = bool(torch.any(vals != 0))
+            zp = FileRange(wf, z[0], 4 * out_dim) if nonzero else None
+        b.add_dequant_file(offset, FileRange(wf, q_off, out_dim * ld), out_dim, ld, in_flat,
+                           FileRange(wf, s_off, 4 * out_dim), zp)
+        return True
 
     # ── module-backed direct load ────────────────────────────────────
 

@@ -7,9 +7,11 @@ and loads the layer tensors through an external package
 tensor naming used here is therefore this build's: a manifest layer may name
 its tensors with ``qweight_key``, ``scale_key``, ``zero_point_key`` and
 ``bias_key``; otherwise they are ``<canonical_name>.qweight`` / ``.scale`` /
-``.zero_point``, and a missing zero point means zeros. Tensors are zero-copy
-views of the memory-mapped file, so the loader's host copy reads the mapped
-pages directly into the pinned slab.
+``.zero_point``, and a missing zero point means zeros. ``read_v2_layers``
+gives zero-copy views of the memory-mapped file (the loader's host copy reads
+the mapped pages into the pinned slab); ``read_v2_locations`` gives each
+tensor's byte range in the file instead, for the native weight-file reader,
+which reads the int8 rows and scales straight into the slab.
 """
 from __future__ import annotations
 
@@ -22,35 +24,45 @@ import torch
 
 from stagehand_amd.registry import parse_safetensors_index
 
-__all__ = ["read_v2_layers", "write_v2_slab"]
+__all__ = ["read_v2_layers", "read_v2_locations", "write_v2_slab"]
+
+# (file offset, bytes, dtype, shape) of one tensor
+Location = tuple[int, int, torch.dtype, tuple[int, ...]]
 
 
-def read_v2_layers(safetensors_path: str, manifest_path: str, file_view: memoryview) -> dict[str, dict[str, Any]]:
+def read_v2_locations(safetensors_path: str, manifest_path: str) -> dict[str, dict[str, Location]]:
+    """layer → {"qweight", "scale", ["zero_point"], ["bias"]} → where the tensor lies in the file."""
     index = parse_safetensors_index(Path(safetensors_path))
     manifest = json.loads(Path(manifest_path).read_text())
-
-    def tensor(key: str | None) -> torch.Tensor | None:
-        if not key or key not in index:
-            return None
-        off, nbytes, dtype, shape = index[key]
-        with warnings.catch_warnings():
-            warnings.simplefilter("ignore", UserWarning)
-            return torch.frombuffer(file_view[off:off + nbytes], dtype=dtype).reshape(shape)
-
-    layers: dict[str, dict[str, Any]] = {}
+    layers: dict[str, dict[str, Location]] = {}
     for entry in manifest.get("layers", []):
         name = entry.get("canonical_name", "")
         if not name:
             continue
-        q = tensor(entry.get("qweight_key", f"{name}.qweight"))
-        s = tensor(entry.get("scale_key", f"{name}.scale"))
-        z = tensor(entry.get("zero_point_key", f"{name}.zero_point"))
-        if z is None and s is not None:
-            z = torch.zeros(s.numel(), dtype=torch.float32)
-        layer: dict[str, Any] = {"qweight": q, "scale": s, "zero_point": z}
-        b = tensor(entry.get("bias_key"))
-        if b is not None:
-            layer["bias"] = b
+        keys = {"qweight": entry.get("qweight_key", f"{name}.qweight"),
+                "scale": entry.get("scale_key", f"{name}.scale"),
+                "zero_point": entry.get("zero_point_key", f"{name}.zero_point"),
+                "bias": entry.get("bias_key")}
+        layers[name] = {what: tuple(index[k]) for what, k in keys.items() if k and k in index}
+    return layers
+
+
+def read_v2_layers(safetensors_path: str, manifest_path: str, file_view: memoryview) -> dict[str, dict[str, Any]]:
+    """layer → {"qweight", "scale", "zero_point", ["bias"]} as views of the mapped file (a
+    missing zero point is zeros), the layer dict of src/stagehand/scheduler.py:285-308."""
+    layers: dict[str, dict[str, Any]] = {}
+    for name, loc in read_v2_locations(safetensors_path, manifest_path).items():
+        views: dict[str, Any] = {}
+        for what, (off, nbytes, dtype, shape) in loc.items():
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore", UserWarning)
+                views[what] = torch.frombuffer(file_view[off:off + nbytes], dtype=dtype).reshape(shape)
+        s = views.get("scale")
+        layer: dict[str, Any] = {"qweight": views.get("qweight"), "scale": s, "zero_point": views.get("zero_point")}
+        if layer["zero_point"] is None and s is not None:
+            layer["zero_point"] = torch.zeros(s.numel(), dtype=torch.float32)
+        if "bias" in views:
+            layer["bias"] = views["bias"]
         layers[name] = layer
     return layers
 

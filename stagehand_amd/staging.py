@@ -78,8 +78,8 @@ class SourceBuilder:
     runtime_dtype: torch.dtype
     dst_bytes: int
     _regions: list[tuple] = field(default_factory=list)  # (kind, dst_off, host tensor|None, rows, cols, ld, scale rows)
-    _scales: list[torch.Tensor] = field(default_factory=list)
-    _zps: list[torch.Tensor | None] = field(default_factory=list)
+    _scales: list[Any] = field(default_factory=list)  # per dequant region: fp32 tensor or FileRange
+    _zps: list[Any] = field(default_factory=list)  # per dequant region: fp32 tensor, FileRange or None
     _mutable: list[bool] = field(default_factory=list)  # per region: bytes may change between loads
 
     def __post_init__(self) -> None:
@@ -150,6 +150,28 @@ class SourceBuilder:
         self._zps.append(z)
         self._mutable.append(False)
 
+    def add_dequant_file(self, dst_off: int, q_rows: FileRange, out_dim: int, ld: int, in_flat: int,
+                         scale: FileRange | torch.Tensor, zero_point: FileRange | torch.Tensor | None) -> None:
+        """SquareQ weight read from a file: ``q_rows`` holds ``out_dim`` int8 rows of ``ld`` values
+        (the first ``in_flat`` are used); ``scale`` / ``zero_point`` give ``out_dim`` fp32 values
+        each, as file ranges or host tensors; ``zero_point`` None means zeros."""
+        if in_flat > ld:
+            raise ValueError(f"SquareQ row of {ld} values is shorter than in_features {in_flat}")
+        if q_rows.nbytes != out_dim * ld:
+            raise ValueError(f"int8 range of {q_rows.nbytes} bytes is not {out_dim} rows of {ld}")
+        for what, v in (("scale", scale), ("zero point", zero_point)):
+            if isinstance(v, FileRange) and v.nbytes != 4 * out_dim:
+                raise ValueError(f"{what} range of {v.nbytes} bytes does not hold {out_dim} fp32 values")
+        kind = KIND_I8_ROWSCALE_BF16 if self.runtime_dtype == torch.bfloat16 else KIND_I8_ROWSCALE_F32
+        if not isinstance(scale, FileRange):
+            scale = _host_contig(scale).reshape(-1)[:out_dim].to(torch.float32)
+        if zero_point is not None and not isinstance(zero_point, FileRange):
+            zero_point = _host_contig(zero_point).reshape(-1)[:out_dim].to(torch.float32)
+        self._regions.append((kind, dst_off, q_rows, out_dim, in_flat, ld, out_dim))
+        self._scales.append(scale)
+        self._zps.append(zero_point)
+        self._mutable.append(False)
+
     # ── layout ───────────────────────────────────────────────────────
 
     def finish(self) -> tuple[BlockSource, np.ndarray | None]:
@@ -168,7 +190,11 @@ class SourceBuilder:
         mutable = set()
         rows: list[tuple] = []
         cursor = 0
-        scale_row = 0
+        # scale rows follow the dequant regions in the order they were added (the order of _scales)
+        first_row, scale_row = [], 0
+        for r in self._regions:
+            first_row.append(scale_row)
+            scale_row += r[6]
         # file ranges go first, in file order, so that neighbours in the file are
         # neighbours in the slab (one read each run); the rest keep their order
         order = sorted(range(len(self._regions)), key=lambda i: (
@@ -195,24 +221,47 @@ class SourceBuilder:
                     mutable.add(len(pieces))
                 pieces.append((off, t))
                 cursor = off + t.numel()
-            rows.append((kind, off, dst_off, r, c, ld, scale_row))
-            scale_row += srows
+            rows.append((kind, off, dst_off, r, c, ld, first_row[i]))
         scale_off = zp_off = -1
         if self._scales:
+            counts = [s.nbytes // 4 if isinstance(s, FileRange) else s.numel() for s in self._scales]
             scale_off = _align(cursor)
-            scales = torch.cat(self._scales)
-            pieces.append((scale_off, scales.view(torch.uint8)))
-            cursor = scale_off + scales.numel() * 4
-            if any(z is not None and bool(torch.any(z != 0)) for z in self._zps):
+            pieces.extend(_row_pieces(scale_off, self._scales, counts))
+            cursor = scale_off + 4 * sum(counts)
+            # a zero-point range counts as non-zero (the caller passes None for all-zero ones)
+            if any(isinstance(z, FileRange) or (z is not None and bool(torch.any(z != 0))) for z in self._zps):
                 zp_off = _align(cursor)
-                zps = torch.cat([z if z is not None else torch.zeros_like(s) for z, s in zip(self._zps, self._scales)])
-                pieces.append((zp_off, zps.view(torch.uint8)))
-                cursor = zp_off + zps.numel() * 4
+                zps = [z if z is not None else torch.zeros(n, dtype=torch.float32) for z, n in zip(self._zps, counts)]
+                pieces.extend(_row_pieces(zp_off, zps, counts))
+                cursor = zp_off + 4 * sum(counts)
         descs = make_descs(rows)
         key = descs.tobytes() + f"|{scale_off}|{zp_off}|{cursor}".encode()
         src = BlockSource(pieces=pieces, src_bytes=max(cursor, 1), scale_off=scale_off, zp_off=zp_off,
                           n_scale=scale_row, key=key, mutable=frozenset(mutable))
         return src, descs
+
+
+def _row_pieces(base: int, values: list[Any], counts: list[int]) -> list[tuple[int, Any]]:
+    """Per-row fp32 vectors back to back from ``base``: host tensors merge into one piece per
+    run, file ranges stay pieces of their own."""
+    out: list[tuple[int, Any]] = []
+    run: list[torch.Tensor] = []
+    run_off = off = base
+    for v, n in zip(values, counts):
+        if isinstance(v, FileRange):
+            if run:
+                out.append((run_off, torch.cat(run).view(torch.uint8)))
+                run = []
+            out.append((off, v))
+            run_off = off + 4 * n
+        else:
+            if not run:
+                run_off = off
+            run.append(v)
+        off += 4 * n
+    if run:
+        out.append((run_off, torch.cat(run).view(torch.uint8)))
+    return out
 
 
 class PlanCache:

@@ -16,11 +16,12 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.squareq import cast_f32_bf16
+from oracle.squareq import cast_f32_bf16, dequant_rows
 from stagehand_amd import _native
 from stagehand_amd.fileio import ALIGN, FileCache, FileRange, WeightFile
 from stagehand_amd.staging import SourceBuilder
-from stagehand_amd.unpack import KIND_BF16_F32, KIND_COPY_BYTES, KIND_F32_BF16, KIND_ZERO_BYTES
+from stagehand_amd.unpack import (KIND_BF16_F32, KIND_COPY_BYTES, KIND_F32_BF16, KIND_I8_ROWSCALE_BF16,
+                                  KIND_ZERO_BYTES)
 
 
 def _aligned(nbytes: int, misalign: int = 0) -> tuple[np.ndarray, torch.Tensor]:
@@ -163,12 +164,20 @@ def test_errors(blob, tmp_path):
     cache.close()
 
 
-def _apply_descs(slab: np.ndarray, descs: np.ndarray, dst_bytes: int) -> np.ndarray:
-    """CPU application of a copy / cast / zero descriptor table (the unpack kernel's contract)."""
+def _apply_descs(slab: np.ndarray, descs: np.ndarray, dst_bytes: int, scale_off: int = -1,
+                 zp_off: int = -1) -> np.ndarray:
+    """CPU application of a descriptor table (the unpack kernel's contract); the int8 rows use
+    the oracle's dequant with the per-row scales / zero points the table points at."""
     out = np.zeros(dst_bytes, dtype=np.uint8)
     for d in descs:
         kind, s, o, n = int(d["kind"]), int(d["src_off"]), int(d["dst_off"]), int(d["rows"]) * int(d["cols"])
-        if kind == KIND_COPY_BYTES:
+        if kind == KIND_I8_ROWSCALE_BF16:
+            rows, cols, ld, r0 = int(d["rows"]), int(d["cols"]), int(d["src_ld"]), int(d["scale_off"])
+            q = slab[s:s + rows * ld].view(np.int8).reshape(rows, ld)
+            sc = slab[scale_off + 4 * r0:scale_off + 4 * (r0 + rows)].copy().view(np.float32)
+            zp = None if zp_off < 0 else slab[zp_off + 4 * r0:zp_off + 4 * (r0 + rows)].copy().view(np.float32)
+            out[o:o + 2 * n] = dequant_rows(q, sc, zp, rows, cols).astype("<u2").reshape(-1).view(np.uint8)
+        elif kind == KIND_COPY_BYTES:
             out[o:o + n] = slab[s:s + n]
         elif kind == KIND_ZERO_BYTES:
             out[o:o + n] = 0
@@ -232,6 +241,78 @@ def test_builder_file_layout(tmp_path, direct):
     _native.call("sh_file_read_batch", r.ctypes.data, 1, slab.data_ptr(), 4)
     out = _apply_descs(slab.numpy(), descs, dst_off)
     assert out.tobytes() == bytes(want)
+    f.close()
+
+
+def _slab_bytes(src) -> np.ndarray:
+    """The source slab a loader would assemble: host pieces copied, file ranges read."""
+    _keep, slab = _aligned(src.src_bytes)
+    out = slab.numpy()
+    for off, p in src.pieces:
+        if isinstance(p, FileRange):
+            p.file.read_into(torch.from_numpy(out[off:off + p.nbytes]), p.offset, p.nbytes)
+        else:
+            out[off:off + p.numel() * p.element_size()] = p.reshape(-1).view(torch.uint8).numpy()
+    return out.copy()
+
+
+@pytest.mark.parametrize("direct", [False, True])
+def test_builder_squareq_v2_file_regions(tmp_path, direct):
+    """SquareQ V2 layers as file ranges (int8 rows, scales, zero points) give the bytes of the same
+    layers as host tensors, and those of the oracle's dequant of src/stagehand/scheduler.py:285-300."""
+    from stagehand_amd.squareq_v2 import read_v2_layers, read_v2_locations, write_v2_slab
+
+    g = torch.Generator().manual_seed(9)
+    spec = {"a": (40, 33, 40, True), "b": (17, 64, 64, False), "c": (9, 5, 8, None)}  # out, in, ld, zp
+    layers = {}
+    for name, (out_f, in_f, ld, zp) in spec.items():
+        t = {"qweight": torch.randint(-127, 128, (out_f, ld), dtype=torch.int8, generator=g),
+             "scale": torch.exp(torch.randn(out_f, generator=g) * 0.5 - 6.0), "in_features": in_f,
+             "bias": torch.randn(out_f, generator=g).to(torch.bfloat16)}
+        if zp is not None:
+            t["zero_point"] = torch.randn(out_f, generator=g) if zp else torch.zeros(out_f)
+        layers[name] = t
+    path = str(tmp_path / "slab.safetensors")
+    manifest = write_v2_slab(path, layers)
+    views = read_v2_layers(path, manifest, memoryview(open(path, "rb").read()))
+    locs = read_v2_locations(path, manifest)
+    f = WeightFile(path, direct=direct)
+    module_norm = torch.randn(24, generator=g)  # fp32 module parameter between the layers
+    builders = [SourceBuilder(torch.bfloat16, 0), SourceBuilder(torch.bfloat16, 0)]
+    want = bytearray()
+    for bi, b in enumerate(builders):
+        dst = 0
+        for name, (out_f, in_f, ld, zp) in spec.items():
+            if bi == 0:
+                L = views[name]
+                b.add_dequant(dst, L["qweight"], in_f, L["scale"], L["zero_point"])
+            else:
+                q, s_, z = locs[name]["qweight"], locs[name]["scale"], locs[name].get("zero_point")
+                zr = FileRange(f, z[0], z[1]) if (z is not None and zp) else None
+                b.add_dequant_file(dst, FileRange(f, q[0], q[1]), out_f, ld, in_f, FileRange(f, s_[0], s_[1]), zr)
+            dst += out_f * in_f * 2
+            if bi == 0:
+                b.add_param(dst, views[name]["bias"])
+            else:
+                bl = locs[name]["bias"]
+                assert b.add_file_param(dst, FileRange(f, bl[0], bl[1]), bl[2], out_f)
+            dst += out_f * 2
+            b.add_param(dst, module_norm, mutable=True)
+            dst += 24 * 2
+            if bi == 0:
+                L = layers[name]
+                want += dequant_rows(L["qweight"].numpy(), L["scale"].numpy(),
+                                     L["zero_point"].numpy() if "zero_point" in L else None,
+                                     out_f, in_f).astype("<u2").tobytes()
+                want += L["bias"].view(torch.uint8).numpy().tobytes()
+                want += cast_f32_bf16(module_norm.numpy()).astype("<u2").tobytes()
+        b.dst_bytes = dst
+    outs = []
+    for b in builders:
+        src, descs = b.finish()
+        outs.append(_apply_descs(_slab_bytes(src), descs, b.dst_bytes, src.scale_off, src.zp_off).tobytes())
+    assert outs[0] == bytes(want)
+    assert outs[1] == bytes(want)
     f.close()
 
 
@@ -408,4 +489,65 @@ def test_pinned_images_survive_module_params_changing_dtype(tmp_path, reader):
         (f,) = rt.scheduler._weight_files.files()
         info = f.info()
         assert info["bytes_direct"] + info["bytes_bounced"] + info["bytes_buffered"] <= f.size
+    rt.shutdown()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("reader", ["mmap", "pread", "direct"])
+@pytest.mark.parametrize("padded,with_zp", [(0, False), (16, True)])
+def test_squareq_v2_streaming_per_reader(tmp_path, reader, padded, with_zp):
+    """A SquareQ V2 slab (safetensors + manifest) streamed with each reader gives the host dequant
+    of src/stagehand/scheduler.py:285-308 bit for bit; with the native readers the int8 rows,
+    scales and zero points are read from the file straight into the pinned slab."""
+    import stagehand_amd as stagehand
+    from stagehand_amd.squareq_v2 import write_v2_slab
+    from tests.streaming_models import TinyStack, expected_squareq_weight, init_, squareq_payload
+
+    model = init_(TinyStack(n=4, hidden=96, mlp=4))
+    payload = squareq_payload(model, padded=padded, with_zp=with_zp)
+    layers = {}
+    for name, L in payload["layers"].items():
+        t = {"qweight": L["qweight"], "scale": L["scale"], "bias": L["bias"], "in_features": L["qweight"].shape[1] - padded}
+        if with_zp:
+            t["zero_point"] = L["zero_point"]
+        layers[name] = t
+    path = tmp_path / "tiny.safetensors"
+    manifest = write_v2_slab(str(path), layers)
+    model.requires_grad_(False)
+    ref = init_(TinyStack(n=4, hidden=96, mlp=4))
+    for bi, blk in enumerate(ref.blocks):
+        for lname in ("fc1", "fc2"):
+            lin = getattr(blk, lname)
+            L = payload["layers"][f"blocks.{bi}.{lname}"]
+            with torch.no_grad():
+                lin.weight.copy_(expected_squareq_weight(L, *lin.weight.shape, torch.bfloat16).float())
+                lin.bias.copy_(L["bias"].to(torch.bfloat16).float())
+    ref = ref.to(device="cuda", dtype=torch.bfloat16)
+    model = model.to(torch.bfloat16)
+    base_mb = torch.cuda.memory_allocated() / 2**20
+    cfg = _config(file_reader=reader, vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb),
+                  prefetch_window_blocks=1)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                    inference_mode=True)
+    assert rt.convert_registry_to_squareq_v2_backed(str(path), manifest) == 4 * 4
+    x = torch.randn(5, 96).to(torch.bfloat16).cuda()
+    outs = []
+    for step in range(3):
+        rt.begin_step(step)
+        with torch.no_grad(), rt.managed_forward():
+            outs.append(model(x))
+        rt.end_step()
+    with torch.no_grad():
+        want = ref(x)
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.equal(_bits(y), _bits(want))
+    assert sum(m.evictions for m in rt.telemetry.history) > 0
+    if reader != "mmap":
+        (f,) = rt.scheduler._weight_files.files()
+        info = f.info()
+        read = info["bytes_direct"] + info["bytes_bounced"] + info["bytes_buffered"]
+        int8 = sum(L["qweight"].numel() - padded * L["qweight"].shape[0] for L in payload["layers"].values())
+        assert read >= int8  # every step's int8 rows came through the reader
+        assert not rt.scheduler._squareq_layers  # no host views of the slab were made
     rt.shutdown()
