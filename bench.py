@@ -234,7 +234,7 @@ def write_dit_safetensors_sharded(model, directory: Path, seed: int) -> int:
 def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
     import stagehand_amd as stagehand
 
-    if kind == "squareq":
+    if kind.startswith("squareq"):
         # 6 GB steady-state cap: the high watermark leaves room for the prefetch
         # window's blocks and their int8 staging buffers on top of it (measured:
         # window 2, watermarks 3.8 / 2.8 GB keep the peak under 6 GB while the
@@ -331,7 +331,9 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
 
     rt = stagehand.StagehandRuntime(model, _dit_config(kind, args, pinned, reader), block_pattern=DIT_BLOCK_PATTERN,
                                     dtype=torch.bfloat16, inference_mode=True)
-    if kind == "squareq":
+    if kind == "squareq_v2":
+        converted = rt.convert_registry_to_squareq_v2_backed(str(src), str(src.with_suffix(".manifest.json")))
+    elif kind == "squareq":
         converted = rt.convert_registry_to_file_backed(str(src))
     else:
         converted = rt.convert_registry_to_file_backed_sharded(str(src))
@@ -375,10 +377,11 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
                 break
     res = {
         "source_mode": "pinned source images" if pinned else "bounded pinned pool (staged)",
-        "file_reader": reader if kind == "file" else None,
+        "file_reader": reader if kind in ("file", "squareq_v2") else None,
         "params_converted": converted,
-        "int8_elements": sum(l.in_features * l.out_features for _n, l in dit_linear_layers(model)) if kind == "squareq" else None,
-        "scale_rows": sum(l.out_features for _n, l in dit_linear_layers(model)) if kind == "squareq" else None,
+        "int8_elements": (sum(l.in_features * l.out_features for _n, l in dit_linear_layers(model))
+                          if kind.startswith("squareq") else None),
+        "scale_rows": sum(l.out_features for _n, l in dit_linear_layers(model)) if kind.startswith("squareq") else None,
         "block_bf16_bytes_per_step": bf16_bytes,
         "pcie_bytes_per_step": sent // args.dit_steps,
         "ms_per_step": round(ms, 2),
@@ -820,6 +823,18 @@ def dit_leg(kind: str, args) -> dict:
         torch.cuda.empty_cache()
     if kind == "file" and args.readers == "on":
         res["readers"] = readers_leg(args, src, reader)
+    if kind == "squareq" and args.squareq_v2 == "on":
+        from stagehand_amd.squareq_v2 import write_v2_slab
+
+        v2 = workdir / "dit_v2.safetensors"
+        t0 = time.perf_counter()
+        write_v2_slab(str(v2), {n: {"qweight": L["qweight"], "scale": L["scale"], "bias": L["bias"]}
+                                for n, L in layers.items()})  # zero points are all 0: left out
+        log(f"dit/squareq: wrote the V2 slab in {time.perf_counter() - t0:.1f}s; streaming it (reader {args.file_reader})")
+        r = _dit_run("squareq_v2", args, v2, layers, False, args.file_reader)
+        res["v2"] = {k: r[k] for k in ("file_reader", "ms_per_step", "streamed_gbps", "pcie_bytes_per_step",
+                                       "peak_vram_gb", "weight_check", "out_finite", "timeline")}
+        torch.cuda.empty_cache()
     best = min((res[m] for m in ("staged", "pinned") if m in res), key=lambda r: r["ms_per_step"])
     for k in ("ms_per_step", "streamed_gbps", "pcie_bytes_per_step", "block_bf16_bytes_per_step", "int8_elements",
               "scale_rows", "peak_vram_gb"):
@@ -895,6 +910,8 @@ def main() -> int:
                     help="weight-file reader of the config-3 leg")
     ap.add_argument("--readers", default="on", choices=["on", "off"],
                     help="config-3 shards through every file reader, cold and warm page cache")
+    ap.add_argument("--squareq-v2", default="on", choices=["on", "off"],
+                    help="config 4 also from a SquareQ V2 slab (safetensors + manifest) through the file reader")
     ap.add_argument("--train-steps", type=int, default=2)
     ap.add_argument("--train-warmup", type=int, default=1)
     args = ap.parse_args()
