@@ -173,6 +173,60 @@ def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
     }
 
 
+def cpu_reference_config4_step(seed: int) -> dict:
+    """The reference's config-4 block load timed on a sample: for one double-stream and one
+    single-stream block of the 12B DiT, the torch CPU dequant of every Linear into a pinned bf16
+    slab (scheduler.py:290-300) and the bias copies, then the bf16 H2D and its wait, one block after
+    another as the reference's hook thread does (scheduler.py:953-1031, 1089-1120). The step is
+    scaled from the two blocks (19 double + 38 single); synthetic int8 values of the DiT's shapes."""
+    import torch
+
+    from oracle.torch_ref import host_dequant_into
+    from stagehand_amd.workloads import FluxStyleDiT, dit_linear_layers
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    with torch.device("meta"):
+        model = FluxStyleDiT(depth_double=1, depth_single=1)
+    g = torch.Generator().manual_seed(seed)
+    out: dict = {"cores": threads, "kind": "port"}
+    for kind in ("double_blocks.0", "single_blocks.0"):
+        lins = [(n, m) for n, m in dit_linear_layers(model) if n.startswith(kind + ".")]
+        work, biases, pos = [], [], 0
+        for _n, lin in lins:
+            o, i = lin.out_features, lin.in_features
+            q = torch.randint(-127, 128, (o, i), dtype=torch.int8, generator=g)
+            sc = torch.exp(torch.randn(o, generator=g) * 0.5 - 6.0)
+            work.append((pos, q, sc, torch.zeros(o), o, i))
+            pos += o * i * 2
+            biases.append((pos, (torch.randn(o, generator=g) * 0.02).to(torch.bfloat16)))
+            pos += o * 2
+        slab = torch.empty(pos, dtype=torch.uint8, pin_memory=True)
+        dev = torch.empty(pos, dtype=torch.uint8, device="cuda")
+        times = []
+        for _rep in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            host_dequant_into(slab, work)
+            for off, b in biases:
+                slab[off:off + b.numel() * 2].copy_(b.view(torch.uint8))
+            t1 = time.perf_counter()
+            dev.copy_(slab, non_blocking=True)
+            torch.cuda.synchronize()
+            times.append((t1 - t0, time.perf_counter() - t1))
+        host_s, h2d_s = sorted(times)[1]
+        out[kind.split(".")[0]] = {"bf16_bytes": pos, "host_dequant_ms": round(host_s * 1e3, 1),
+                                   "h2d_ms": round(h2d_s * 1e3, 1)}
+        del slab, dev, work
+    d, sg = out["double_blocks"], out["single_blocks"]
+    step = 19 * (d["host_dequant_ms"] + d["h2d_ms"]) + 38 * (sg["host_dequant_ms"] + sg["h2d_ms"])
+    out["ms_per_step"] = round(step, 1)
+    out["pcie_bytes_per_step"] = 19 * d["bf16_bytes"] + 38 * sg["bf16_bytes"]
+    out["sample"] = ("one double- and one single-stream block of the 12B DiT (synthetic int8, fp32 row scales), "
+                     "median of 3; step = 19 double + 38 single")
+    return out
+
+
 def _dit_inputs(seed: int, img_tokens: int = 4096, txt_tokens: int = 512, hidden: int = 3072):
     import torch
 
@@ -1042,6 +1096,9 @@ def main() -> int:
     if args.dit in ("squareq", "both"):
         log("dit: config 4 (SquareQ) streaming")
         d = result["dit_squareq"] = dit_leg("squareq", args)
+        if "cpu_baseline" in result:
+            log("cpu baseline: the reference's config-4 block loads on a sample")
+            d["reference_host_dequant_path"] = cpu_reference_config4_step(args.seed)
         if "cpu_baseline" in result and "pcie" in result:
             # The reference's config-4 path dequantises every weight on the host
             # (scheduler.py:290-300, at the CPU-baseline rate measured above) and

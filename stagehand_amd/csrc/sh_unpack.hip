@@ -46,11 +46,12 @@
 
 namespace {
 
-// Launch shape, chosen by measurement on MI355X over the config-2 slab: one
-// chunk per thread and many short-lived 512-thread workgroups stream best
-// (dequant 16 int8 → 32 B of bf16 per thread; cast 4 fp32 → 8 B per thread).
-// Persistent grids, deeper per-thread unrolling, wider cast chunks and
-// non-temporal loads/stores each measured 5-25% slower.
+// Launch shape, chosen by measurement on MI355X over the config-2 slab: a
+// chunk or two per thread and many short-lived 512-thread workgroups stream
+// best (dequant two chunks of 8 int8 → 16 B of bf16 each per thread; cast one
+// chunk of 4 fp32 → 8 B per thread). Persistent grids, deeper per-thread
+// unrolling, wider chunks and non-temporal loads/stores each measured 5-25%
+// slower.
 #ifndef SH_UNPACK_THREADS
 #define SH_UNPACK_THREADS 512
 #endif
