@@ -292,6 +292,12 @@ void worker_loop(sh_loader* L) {
     }
     std::string err;
     const int st = run_request(L, *t, err);
+    if (st != SH_OK) {
+      // Chunks copied before the failure may still be landing in the destination:
+      // mark their end so that releasing the ticket waits for them.
+      (void)hipEventRecord(t->copied, L->copy_stream);
+      (void)hipEventRecord(t->done, L->copy_stream);
+    }
     {
       std::lock_guard<std::mutex> lk(L->mu);
       t->status = st;
@@ -527,12 +533,11 @@ extern "C" int sh_loader_release(sh_loader* L, uint64_t ticket) {
   if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "sh_loader_release: unknown ticket %llu", (unsigned long long)ticket);
   // Never recycle events the worker may still record: wait until it is done with the ticket.
   L->issued_cv.wait(lk, [&] { return it->second.state != TicketState::Queued; });
-  const bool issued = it->second.state == TicketState::Issued;
-  hipEvent_t copied = it->second.copied, done = it->second.done;
+  hipEvent_t done = it->second.done;
   lk.unlock();
-  // Events go back to the spare list only once the device has passed them.
-  hipError_t e = issued ? hipEventSynchronize(done) : hipSuccess;
-  if (e == hipSuccess && !issued) e = hipEventSynchronize(copied);
+  // Events go back to the spare list only once the device has passed them (a
+  // failed ticket's events mark the copies queued before the failure).
+  const hipError_t e = hipEventSynchronize(done);
   lk.lock();
   it = L->tickets.find(ticket);
   if (it != L->tickets.end()) {

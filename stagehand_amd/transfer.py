@@ -466,7 +466,7 @@ class AsyncTransferEngine:
             if st == _native.SH_ERR_NOT_READY:
                 return False
             if st != _native.SH_OK:
-                self._raise_transfer(st, handle.block_id, handle.direction)
+                self._raise_transfer(st, handle.block_id, handle.direction, handle)
             self._complete_handle(handle)
             return True
         if handle.event is None:
@@ -489,7 +489,7 @@ class AsyncTransferEngine:
         if handle.ticket is not None:
             st = _native.lib().sh_loader_stream_wait(self._loader, handle.ticket, sh)
             if st != _native.SH_OK:
-                self._raise_transfer(st, handle.block_id, handle.direction)
+                self._raise_transfer(st, handle.block_id, handle.direction, handle)
         elif handle.event is not None:
             _native.call("sh_stream_wait_event", sh, handle.event.handle)
         handle.device_waited = True
@@ -505,7 +505,7 @@ class AsyncTransferEngine:
         if handle.ticket is not None:
             st = _native.lib().sh_loader_sync(self._loader, handle.ticket)
             if st != _native.SH_OK:
-                self._raise_transfer(st, handle.block_id, handle.direction)
+                self._raise_transfer(st, handle.block_id, handle.direction, handle)
         else:
             handle.event.synchronize()
         self.wait_device(handle)
@@ -568,8 +568,15 @@ class AsyncTransferEngine:
         if status != _native.SH_OK:
             self._raise_transfer(status, block_id, direction)
 
-    def _raise_transfer(self, status: int, block_id: str, direction: str) -> None:
+    def _raise_transfer(self, status: int, block_id: str, direction: str,
+                        handle: TransferHandle | None = None) -> None:
         msg = _native.last_error() or f"status {status}"
+        if handle is not None:
+            # a failed load is finished: later waits, drain() and shutdown() do not raise it again
+            try:
+                self._complete_handle(handle)
+            except Exception:  # noqa: BLE001 — the original failure is the one to report
+                pass
         if status == _native.SH_ERR_INVALID:
             raise ValueError(f"{direction} of block {block_id!r}: {msg}")
         raise TransferError(f"{direction} of block {block_id!r} failed: {msg}")

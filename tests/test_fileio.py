@@ -551,3 +551,54 @@ def test_squareq_v2_streaming_per_reader(tmp_path, reader, padded, with_zp):
         assert read >= int8  # every step's int8 rows came through the reader
         assert not rt.scheduler._squareq_layers  # no host views of the slab were made
     rt.shutdown()
+
+
+def test_builder_rejects_inconsistent_file_ranges(tmp_path):
+    path = tmp_path / "x.bin"
+    np.zeros(4096, dtype=np.uint8).tofile(path)
+    f = WeightFile(path)
+    b = SourceBuilder(torch.bfloat16, 4096)
+    with pytest.raises(ValueError, match="does not hold"):
+        b.add_file_param(0, FileRange(f, 0, 100), torch.bfloat16, 64)
+    with pytest.raises(ValueError, match="not 4 rows"):
+        b.add_dequant_file(0, FileRange(f, 0, 100), 4, 32, 32, FileRange(f, 0, 16), None)
+    with pytest.raises(ValueError, match="shorter than"):
+        b.add_dequant_file(0, FileRange(f, 0, 128), 4, 32, 33, FileRange(f, 0, 16), None)
+    with pytest.raises(ValueError, match="scale range"):
+        b.add_dequant_file(0, FileRange(f, 0, 128), 4, 32, 32, FileRange(f, 0, 12), None)
+    with pytest.raises(ValueError, match="zero point range"):
+        b.add_dequant_file(0, FileRange(f, 0, 128), 4, 32, 32, FileRange(f, 0, 16), FileRange(f, 0, 8))
+    f.close()
+
+
+@pytest.mark.gpu
+def test_load_errors_are_reported_and_finish_the_load(tmp_path):
+    """A range past the end of its file is refused at submit (ValueError); a file that shrinks
+    after it was opened fails the load with the read error (TransferError), and the failed load
+    is finished: later waits and shutdown do not raise it again."""
+    from stagehand_amd.errors import TransferError
+    from stagehand_amd.pool import PinnedPool
+    from stagehand_amd.transfer import AsyncTransferEngine, BlockSource
+
+    path = tmp_path / "w.bin"
+    data = np.random.default_rng(1).integers(0, 256, size=3 << 20, dtype=np.uint8)
+    data.tofile(path)
+    f = WeightFile(path)
+    pool = PinnedPool(total_mb=8, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool)
+    dst = torch.empty(2 << 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="past the end"):
+        eng.submit_block_load("b", BlockSource([(0, FileRange(f, data.size - 8, 16))], 16), dst)
+    h = eng.submit_block_load("ok", BlockSource([(0, FileRange(f, 4096, 2 << 20))], 2 << 20), dst)
+    eng.wait(h)
+    assert np.array_equal(dst.cpu().numpy(), data[4096:4096 + (2 << 20)])
+    with open(path, "r+b") as fh:
+        fh.truncate(1 << 20)
+    h = eng.submit_block_load("short", BlockSource([(0, FileRange(f, 0, 2 << 20))], 2 << 20), dst)
+    with pytest.raises(TransferError, match="unexpected end of file"):
+        eng.wait(h)
+    eng.wait(h)  # finished: no second error
+    assert eng.inflight_count() == 0
+    eng.shutdown()
+    pool.shutdown()
+    f.close()
