@@ -352,3 +352,48 @@ def test_checkpointed_lora_training_round_trip(frozen_host_copies):
     else:
         assert sent_back >= evictions * frozen_per_block
     rt.shutdown()
+
+
+class _SimpleMLP(torch.nn.Module):
+    def __init__(self, hidden: int = 16, num_layers: int = 3) -> None:
+        super().__init__()
+        self.layers = torch.nn.ModuleList(torch.nn.Linear(hidden, hidden, bias=False) for _ in range(num_layers))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        for layer in self.layers:
+            x = layer(x)
+        return x
+
+
+@pytest.mark.parametrize("inference_mode", [False, True])
+def test_layer_mode_fp32_matches_unwrapped(inference_mode):
+    """Layer mode with fp32 storage gives the unwrapped model's outputs on the trace step, the
+    scheduled step and later steps, and gradients on every managed parameter (the checks of the
+    reference's tests/test_compat_ramtorch.py:263-340, through stagehand.layer)."""
+    torch.manual_seed(3)
+    model = _SimpleMLP(hidden=64, num_layers=4)
+    ref = _SimpleMLP(hidden=64, num_layers=4)
+    ref.load_state_dict(model.state_dict())
+    ref = ref.cuda()
+    x = torch.randn(2, 64, device="cuda")
+    m = stagehand.layer(model, dtype=torch.float32, inference_mode=inference_mode, telemetry=False)
+    rt = m._stagehand_layer_runtime
+    try:
+        with torch.no_grad():
+            want = ref(x)
+            outs = [m(x) for _ in range(5)]
+        for i, y in enumerate(outs):
+            assert torch.allclose(y, want, atol=1e-5), f"step {i}"
+        if not inference_mode:
+            for step in range(2):
+                ref.zero_grad(set_to_none=True)
+                ref(x).sum().backward()
+                for p in model.parameters():
+                    p.grad = None
+                m(x).sum().backward()
+                torch.cuda.synchronize()
+                for (name, p), q in zip(model.named_parameters(), ref.parameters()):
+                    assert p.grad is not None, (step, name)
+                    assert torch.allclose(p.grad.to(q.grad.device), q.grad, atol=1e-5), (step, name)
+    finally:
+        rt.shutdown()
