@@ -227,6 +227,66 @@ def cpu_reference_config4_step(seed: int) -> dict:
     return out
 
 
+def cpu_reference_config3_step(src: Path) -> dict:
+    """The reference's config-3 block load timed on a sample: for one double-stream and one
+    single-stream shard, ``copy_`` of every tensor from a ``torch.frombuffer`` view of the mapped
+    file into a pinned slab (scheduler.py:184-241, 564-601; the mapping stays open and warm across
+    loads, as the reference caches it), then the bf16 H2D and its wait (transfer.py:108-143,
+    scheduler.py:1089-1120). Scaled to 19 + 38 blocks."""
+    import mmap
+    import warnings
+
+    import torch
+
+    from stagehand_amd.registry import parse_safetensors_index
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    out: dict = {"cores": threads, "kind": "reference ops (torch)"}
+    for kind in ("double_blocks", "single_blocks"):
+        path = src / f"{kind}.0.safetensors"
+        index = parse_safetensors_index(path)
+        with open(path, "rb") as fh:
+            mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+            view = memoryview(mm)
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore", UserWarning)
+                tensors = [torch.frombuffer(view[o:o + n], dtype=dt) for o, n, dt, _shape in index.values()]
+            total = sum(t.numel() * t.element_size() for t in tensors)
+            slab = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+            dev = torch.empty(total, dtype=torch.uint8, device="cuda")
+            times = []
+            for _rep in range(4):  # the first pass maps the pages; the rest are the steady state
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                pos = 0
+                for t in tensors:
+                    n = t.numel() * t.element_size()
+                    slab[pos:pos + n].view(t.dtype).copy_(t)
+                    pos += n
+                t1 = time.perf_counter()
+                dev.copy_(slab, non_blocking=True)
+                torch.cuda.synchronize()
+                times.append((t1 - t0, time.perf_counter() - t1))
+            first = times[0]
+            stage_s, h2d_s = sorted(times[1:])[1]
+            out[kind] = {"bf16_bytes": total, "stage_ms": round(stage_s * 1e3, 1), "h2d_ms": round(h2d_s * 1e3, 1),
+                         "first_stage_ms": round(first[0] * 1e3, 1)}
+            del tensors, slab, dev, t  # every view of the mapping, before it is closed
+            view.release()
+            mm.close()
+    d, sg = out["double_blocks"], out["single_blocks"]
+    serial = 19 * (d["stage_ms"] + d["h2d_ms"]) + 38 * (sg["stage_ms"] + sg["h2d_ms"])
+    overlap = max(19 * d["stage_ms"] + 38 * sg["stage_ms"], 19 * d["h2d_ms"] + 38 * sg["h2d_ms"])
+    out["ms_per_step_serial"] = round(serial, 1)
+    out["ms_per_step_overlapped"] = round(overlap, 1)
+    out["pcie_bytes_per_step"] = 19 * d["bf16_bytes"] + 38 * sg["bf16_bytes"]
+    out["sample"] = ("shards double_blocks.0 and single_blocks.0 of the config-3 files, page cache warm, mapping "
+                     "warm; median of 3 after a first pass; step = 19 double + 38 single, serial (the reference "
+                     "stages on the hook thread) and with staging fully overlapped with the H2D")
+    return out
+
+
 def _dit_inputs(seed: int, img_tokens: int = 4096, txt_tokens: int = 512, hidden: int = 3072):
     import torch
 
@@ -740,6 +800,22 @@ def _drop_page_cache(src: Path) -> int:
     return total
 
 
+def _warm_page_cache(src: Path) -> float:
+    """Reads every shard once through the page cache (a warm start for the next run); GB/s."""
+    t0, total = time.perf_counter(), 0
+    for p in sorted(src.glob("*.safetensors")):
+        fd = os.open(p, os.O_RDONLY)
+        try:
+            while True:
+                b = os.read(fd, 64 << 20)
+                if not b:
+                    break
+                total += len(b)
+        finally:
+            os.close(fd)
+    return total / (time.perf_counter() - t0) / 1e9
+
+
 def _sample_read_gbps(src: Path, nbytes: int = 128 << 20) -> float:
     """Read rate of the first ``nbytes`` of the last shard: tells a cold page cache (storage
     rate) from a warm one (memory rate) after a drop."""
@@ -775,7 +851,11 @@ def _first_steps(args, src: Path, reader: str, cold: bool, steps: int = 2, pinne
                                     dtype=torch.bfloat16, inference_mode=True)
     rt.convert_registry_to_file_backed_sharded(str(src))
     img, txt, vec = _dit_inputs(args.seed)
-    file_bytes = _drop_page_cache(src) if cold else sum(p.stat().st_size for p in src.glob("*.safetensors"))
+    if cold:
+        file_bytes = _drop_page_cache(src)
+    else:
+        _warm_page_cache(src)
+        file_bytes = sum(p.stat().st_size for p in src.glob("*.safetensors"))
     sample = _sample_read_gbps(src)
     torch.cuda.synchronize()
     times, sent = [], []
@@ -821,14 +901,15 @@ def readers_leg(args, src: Path, main_reader: str) -> dict:
     import torch
 
     out: dict = {"file_bytes": sum(p.stat().st_size for p in src.glob("*.safetensors"))}
+    # warm runs first: every shard is read through the page cache just before each
+    for reader in ("mmap", "pread"):
+        log(f"dit/file: reader {reader}, warm first steps")
+        out[f"{reader}_warm"] = _first_steps(args, src, reader, cold=False)
     for reader in ("mmap", "pread", "direct"):
         log(f"dit/file: reader {reader}, cold first steps")
         out[f"{reader}_cold"] = _first_steps(args, src, reader, cold=True)
     log("dit/file: reader direct into pinned source images, cold first steps")
     out["direct_pinned_cold"] = _first_steps(args, src, "direct", cold=True, steps=3, pinned=True)
-    for reader in ("mmap", "pread"):
-        log(f"dit/file: reader {reader}, warm first steps")
-        out[f"{reader}_warm"] = _first_steps(args, src, reader, cold=False)
     for reader in ("mmap", "pread"):
         if reader == main_reader:
             continue
@@ -877,6 +958,9 @@ def dit_leg(kind: str, args) -> dict:
         torch.cuda.empty_cache()
     if kind == "file" and args.readers == "on":
         res["readers"] = readers_leg(args, src, reader)
+    if kind == "file" and not args.skip_cpu:
+        log("cpu baseline: the reference's config-3 block loads on a sample")
+        res["reference_staging_path"] = cpu_reference_config3_step(src)
     if kind == "squareq" and args.squareq_v2 == "on":
         from stagehand_amd.squareq_v2 import write_v2_slab
 

@@ -36,12 +36,12 @@ class StagehandConfig:
     # "pread"  — the native reader: each tensor's byte range is read into the
     #            pinned slab on the copy threads, from the page cache where it
     #            holds the file, else in sequential runs from storage; the file
-    #            stays in the page cache for later steps (the default: on a 12B
-    #            DiT its first step from a warm cache took 0.78 s against 6.6 s
-    #            for "mmap", cold 6.4 s against 6.8 s, later steps the same);
+    #            stays in the page cache for later steps, and no mapping is held
+    #            (measured on a 12B DiT: as fast as "mmap", warm or cold);
     # "direct" — the same around the page cache (O_DIRECT), for weights larger
     #            than host memory or read once: every step reads storage, unless
-    #            pinned_source_cache keeps each block's bytes after the first.
+    #            pinned_source_cache keeps each block's bytes after the first
+    #            (then the fastest cold start, and PCIe-bound after it).
     file_reader: str = "pread"
     # module-backed blocks: a frozen parameter (requires_grad False) whose host
     # tensor already has the runtime dtype keeps that tensor while the block is
