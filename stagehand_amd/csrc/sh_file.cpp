@@ -6,12 +6,11 @@
 // src/stagehand/scheduler.py:184-241, 564-601), and the VMM backend fills
 // regions from the same mapping after an madvise(WILLNEED)
 // (src/stagehand/vmm_backend.py:283-291). Here a block's ranges become pread
-// calls of at most 8 MiB, cut at 8 MiB file offsets and run in parallel, so a
-// hot file is copied out of the page cache by every copy thread without
-// touching a mapping (a fresh mapping costs a page fault per 4 KiB page on
-// first touch). Buffered pieces are read in two phases: every thread first
-// copies what the page cache already holds (preadv2 with RWF_NOWAIT), then
-// the remainders, sorted by file and offset, are cut into up to kColdStreams
+// calls of at most 8 MiB, cut at 8 MiB file offsets and run in parallel: a
+// hot file is copied out of the page cache by every copy thread, holding no
+// mapping of it (copying from a mapping measured as fast). Buffered pieces are
+// read in two phases: every thread first copies what the page cache already
+// holds (preadv2 with RWF_NOWAIT), then the remainders, sorted by file and offset, are cut into up to kColdStreams
 // contiguous runs of about equal size, each read front to back by one thread
 // on a descriptor of its own, so that each run is a sequential stream to the
 // kernel's read-ahead (which is kept per open file). Interleaved cold reads
