@@ -67,25 +67,50 @@ def measured_traffic(kernel: str) -> float | None:
         return None
 
 
-def pinned_h2d_gbps(reps: int = 10, nbytes: int = 1 << 30) -> float:
+def pinned_h2d_gbps(reps: int = 10, nbytes: int = 1 << 30, d2h: bool = False) -> float:
+    """Pinned hipMemcpyAsync rate (1 GiB x 10), host to device or, with ``d2h``, back."""
     import torch
 
     host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
     host.fill_(1)
     dev = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     stream = torch.cuda.Stream()
+    src, dst = (dev, host) if d2h else (host, dev)
     with torch.cuda.stream(stream):
-        dev.copy_(host, non_blocking=True)
+        dst.copy_(src, non_blocking=True)
     stream.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     with torch.cuda.stream(stream):
         for _ in range(reps):
-            dev.copy_(host, non_blocking=True)
+            dst.copy_(src, non_blocking=True)
     t1.record(stream)
     stream.synchronize()
     return reps * nbytes / (t0.elapsed_time(t1) * 1e-3) / 1e9
+
+
+def duplex_gbps(nbytes: int = 1 << 30, reps: int = 10) -> dict:
+    """Pinned H2D and D2H at the same time on two streams: each direction's rate."""
+    import torch
+
+    hs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+    ds = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2)]
+    torch.cuda.synchronize()
+    for i, (st, (a, b)) in enumerate(zip(streams, ev)):
+        a.record(st)
+        with torch.cuda.stream(st):
+            for _ in range(reps):
+                if i == 0:
+                    ds[0].copy_(hs[0], non_blocking=True)
+                else:
+                    hs[1].copy_(ds[1], non_blocking=True)
+        b.record(st)
+    torch.cuda.synchronize()
+    return {"h2d_gbps": round(reps * nbytes / (ev[0][0].elapsed_time(ev[0][1]) * 1e-3) / 1e9, 2),
+            "d2h_gbps": round(reps * nbytes / (ev[1][0].elapsed_time(ev[1][1]) * 1e-3) / 1e9, 2)}
 
 
 def d2d_copy_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
@@ -432,6 +457,14 @@ def timeline_stats(trace: dict, pcie_peak_gbps: float | None) -> dict:
     }
     if pcie_peak_gbps:
         res["h2d_frac_of_measured_pcie_while_copying"] = round(res["h2d_gbps_while_copying"] / pcie_peak_gbps, 4)
+    d2h = trace.get("d2h") or []
+    if d2h:
+        d2h_iv = _union([(a, b) for _n, a, b, *_k in d2h])
+        d2h_ms = _length(d2h_iv)
+        res["d2h_busy_ms"] = round(d2h_ms, 2)
+        res["d2h_gbps_while_copying"] = round(sum(d[0] for d in d2h) / (d2h_ms * 1e-3) / 1e9, 2) if d2h_ms else None
+        res["d2h_h2d_overlap_ms"] = round(_intersect(d2h_iv, copy_iv), 2)
+        res["d2h_span_ms"] = [round(min(d[1] for d in d2h) - span0, 1), round(max(d[2] for d in d2h) - span0, 1)]
     return res
 
 
@@ -1050,8 +1083,8 @@ def main() -> int:
                     help="config-3 shards through every file reader, cold and warm page cache")
     ap.add_argument("--squareq-v2", default="on", choices=["on", "off"],
                     help="config 4 also from a SquareQ V2 slab (safetensors + manifest) through the file reader")
-    ap.add_argument("--train-steps", type=int, default=2)
-    ap.add_argument("--train-warmup", type=int, default=1)
+    ap.add_argument("--train-steps", type=int, default=3)
+    ap.add_argument("--train-warmup", type=int, default=2)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1073,7 +1106,8 @@ def main() -> int:
         return profile_pass(args)
     if args.only_dit:
         args.pcie_peak_gbps = round(pinned_h2d_gbps(), 2)
-        out = {"pcie": {"h2d_pinned_gbps": args.pcie_peak_gbps}}
+        out = {"pcie": {"h2d_pinned_gbps": args.pcie_peak_gbps, "d2h_pinned_gbps": round(pinned_h2d_gbps(d2h=True), 2),
+                        "duplex": duplex_gbps()}}
         if args.dit in ("squareq", "both"):
             out["dit_squareq"] = dit_leg("squareq", args)
         if args.dit in ("file", "both"):
@@ -1168,7 +1202,9 @@ def main() -> int:
         log("d2d copy and pinned H2D")
         result["d2d_copy_gbps"] = round(d2d_copy_gbps(), 2)
         result["copy_kernel_gbps"] = round(copy_kernel_gbps(), 2)
-        result["pcie"] = {"h2d_pinned_gbps": round(pinned_h2d_gbps(), 2), "transfer_bytes": 1 << 30, "reps": 10}
+        result["pcie"] = {"h2d_pinned_gbps": round(pinned_h2d_gbps(), 2),
+                          "d2h_pinned_gbps": round(pinned_h2d_gbps(d2h=True), 2),
+                          "duplex": duplex_gbps(), "transfer_bytes": 1 << 30, "reps": 10}
         args.pcie_peak_gbps = result["pcie"]["h2d_pinned_gbps"]
 
     # The streamed DiTs budget VRAM with torch.cuda.memory_allocated(): release

@@ -325,6 +325,19 @@ typedef struct sh_load_request {
    * ticket and of the ticket queued after it. */
   const struct sh_file_range* ranges;
   uint64_t n_ranges;
+  /* Optional pieces whose sources are pinned host memory (dst = byte offset
+   * in the source, as for pieces): copied straight from their source to the
+   * device by the copy engine, with no slab and no host copy. The regions of
+   * the other pieces and ranges must not overlap them. */
+  const sh_copy_item* dma;
+  uint64_t n_dma;
+  /* Optional event (hipEvent_t) the copies wait for on the device, e.g. the
+   * device-to-host copy that wrote the pinned sources of `dma` (no reference
+   * counterpart: the reference waits on the host before reading them again).
+   * With a pinned image, the loader's worker waits for it on the host before
+   * copying the dma pieces into the image. It must stay valid until the
+   * ticket is issued. */
+  void* wait_event;
 } sh_load_request;
 
 typedef struct sh_loader sh_loader;

@@ -202,7 +202,7 @@ LOAD_REQUEST_DTYPE = np.dtype([
     ("pieces", "<u8"), ("n_pieces", "<u8"), ("src_bytes", "<u8"), ("plan", "<u8"), ("staging", "<u8"),
     ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
     ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"), ("image", "<u8"),
-    ("ranges", "<u8"), ("n_ranges", "<u8"),
+    ("ranges", "<u8"), ("n_ranges", "<u8"), ("dma", "<u8"), ("n_dma", "<u8"), ("wait_event", "<u8"),
 ])
 
 # Mirrors of `struct sh_file_range` / `struct sh_file_info`.

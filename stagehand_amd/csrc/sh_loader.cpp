@@ -63,6 +63,8 @@ struct Ticket {
   // request
   std::vector<sh_copy_item> pieces;
   std::vector<sh_file_range> ranges;
+  std::vector<sh_copy_item> dma;  // pinned sources copied straight to the device
+  hipEvent_t wait_event = nullptr;
   bool advised = false;
   uint64_t src_bytes = 0;
   const sh_plan* plan = nullptr;
@@ -156,20 +158,31 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   void* h2d_dst = t.plan ? t.staging : t.dst;
   e = hipStreamWaitEvent(L->copy_stream, t.ready, 0);
   if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(ready)");
+  if (t.wait_event != nullptr) {
+    e = hipStreamWaitEvent(L->copy_stream, t.wait_event, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(wait_event)");
+  }
   if (t.start != nullptr) {
     e = hipEventRecord(t.start, L->copy_stream);
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord(start)");
   }
   if (t.image != nullptr) {
     // Pinned source image: refresh the given pieces and ranges, then one DMA straight from it.
-    if (!t.pieces.empty() || !t.ranges.empty()) {
+    if (!t.pieces.empty() || !t.ranges.empty() || !t.dma.empty()) {
       auto f = L->image_fence.find(t.image);
       if (f != L->image_fence.end()) {
         e = hipEventSynchronize(f->second);
         if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize(image fence)");
       }
+      if (!t.dma.empty() && t.wait_event != nullptr) {
+        // the host copies the dma sources into the image: they must be final
+        e = hipEventSynchronize(t.wait_event);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize(wait_event)");
+      }
       std::vector<sh::IoPiece> io;
       for (const sh_copy_item& p : t.pieces)
+        sh::append_copy(io, (uint8_t*)t.image + (uintptr_t)p.dst, p.src, p.bytes);
+      for (const sh_copy_item& p : t.dma)
         sh::append_copy(io, (uint8_t*)t.image + (uintptr_t)p.dst, p.src, p.bytes);
       for (const sh_file_range& r : t.ranges)
         sh::append_read(io, r.file, r.file_off, r.bytes, (uint8_t*)t.image + r.dst);
@@ -198,6 +211,14 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   std::vector<sh::IoPiece> io;
   for (uint64_t c0 = 0; t.image == nullptr && c0 < t.src_bytes; c0 += L->slab_bytes) {
     const uint64_t c1 = std::min<uint64_t>(t.src_bytes, c0 + L->slab_bytes);
+    if (!t.dma.empty()) {
+      // only the regions of gathered pieces and ranges go through slabs
+      bool any = false;
+      for (const sh_copy_item& p : t.pieces)
+        any = any || ((uint64_t)(uintptr_t)p.dst < c1 && (uint64_t)(uintptr_t)p.dst + p.bytes > c0 && p.bytes > 0);
+      for (const sh_file_range& r : t.ranges) any = any || (r.dst < c1 && r.dst + r.bytes > c0 && r.bytes > 0);
+      if (!any) continue;
+    }
     uint32_t slab = 0;
     double waited = 0;
     int st = sh_pool_acquire(L->pool, -1, &slab, &waited);
@@ -224,7 +245,24 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
       sh_pool_release(L->pool, slab);
       return st;
     }
-    e = hipMemcpyAsync((uint8_t*)h2d_dst + c0, slab_ptr, c1 - c0, hipMemcpyHostToDevice, L->copy_stream);
+    if (t.dma.empty()) {
+      e = hipMemcpyAsync((uint8_t*)h2d_dst + c0, slab_ptr, c1 - c0, hipMemcpyHostToDevice, L->copy_stream);
+    } else {
+      // the dma pieces write their own regions: send only what was gathered here
+      std::vector<std::pair<uint64_t, uint64_t>> iv;
+      for (const sh::IoPiece& p : io) {
+        const uint64_t a = (uint64_t)(p.dst - (uint8_t*)slab_ptr);
+        iv.emplace_back(a, a + p.bytes);
+      }
+      std::sort(iv.begin(), iv.end());
+      e = hipSuccess;
+      for (size_t i = 0; i < iv.size() && e == hipSuccess;) {
+        uint64_t a = iv[i].first, b = iv[i].second;
+        for (++i; i < iv.size() && iv[i].first <= b; ++i) b = std::max(b, iv[i].second);
+        e = hipMemcpyAsync((uint8_t*)h2d_dst + c0 + a, (uint8_t*)slab_ptr + a, b - a, hipMemcpyHostToDevice,
+                           L->copy_stream);
+      }
+    }
     if (e != hipSuccess) {
       (void)hipStreamSynchronize(L->copy_stream);
       sh_pool_release(L->pool, slab);
@@ -234,6 +272,13 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
     if (st != SH_OK) {
       err = sh_last_error();
       return st;
+    }
+  }
+  if (t.image == nullptr) {
+    for (const sh_copy_item& p : t.dma) {
+      if (p.bytes == 0) continue;
+      e = hipMemcpyAsync((uint8_t*)h2d_dst + (uintptr_t)p.dst, p.src, p.bytes, hipMemcpyHostToDevice, L->copy_stream);
+      if (e != hipSuccess) return hip_fail(e, "pinned-source H2D copy");
     }
   }
   e = hipEventRecord(t.copied, L->copy_stream);
@@ -307,6 +352,9 @@ void worker_loop(sh_loader* L) {
       t->pieces.shrink_to_fit();
       t->ranges.clear();
       t->ranges.shrink_to_fit();
+      t->dma.clear();
+      t->dma.shrink_to_fit();
+      t->wait_event = nullptr;
     }
     L->issued_cv.notify_all();
   }
@@ -430,6 +478,15 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
     if (end < r.bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: range %llu overflows", (unsigned long long)i);
     need = need > end ? need : end;
   }
+  if (req->n_dma > 0 && req->dma == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: dma is NULL");
+  for (uint64_t i = 0; i < req->n_dma; ++i) {
+    const sh_copy_item& p = req->dma[i];
+    const uint64_t end = (uint64_t)(uintptr_t)p.dst + p.bytes;
+    if (end < p.bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: dma piece %llu overflows", (unsigned long long)i);
+    if (p.bytes > 0 && p.src == nullptr)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: dma piece %llu has no source", (unsigned long long)i);
+    need = need > end ? need : end;
+  }
   if (need > req->src_bytes) return sh::fail(SH_ERR_INVALID, "sh_loader_submit: pieces end at %llu, past src_bytes %llu",
                                              (unsigned long long)need, (unsigned long long)req->src_bytes);
   if (req->plan != nullptr) {
@@ -469,6 +526,8 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   }
   t.pieces.assign(req->pieces, req->pieces + req->n_pieces);
   if (req->n_ranges > 0) t.ranges.assign(req->ranges, req->ranges + req->n_ranges);
+  if (req->n_dma > 0) t.dma.assign(req->dma, req->dma + req->n_dma);
+  t.wait_event = (hipEvent_t)req->wait_event;
   t.src_bytes = req->src_bytes;
   t.plan = req->plan;
   t.staging = req->staging;

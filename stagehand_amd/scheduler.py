@@ -217,6 +217,8 @@ class StagehandScheduler:
         # block → {param name: host tensor} kept for frozen module parameters while
         # the block is resident (config.frozen_host_copies)
         self._host_copies: dict[str, dict[str, torch.Tensor]] = {}
+        # block → pinned host buffer in the block's layout, the target of its whole-block save-backs
+        self._host_homes: dict[str, torch.Tensor] = {}
         # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
         self._done_marks: collections.deque = collections.deque()
 
@@ -292,6 +294,37 @@ class StagehandScheduler:
         if ev is not None:
             prev = self._d2h_fences.get(block_id)
             self._d2h_fences[block_id] = ev if prev is None else ev  # later event covers earlier copies on the stream
+
+    def _save_block_home(self, block_id: str, module: nn.Module, res_entry: ResidencyEntry, names: list[str]) -> bool:
+        """Save-back of a whole module-backed block in one copy into its pinned home buffer.
+
+        Used when every parameter is copied back and is still its view of the block's device
+        buffer: that buffer is then the block's bytes in the layout, so one D2H copies it into
+        a pinned host buffer kept for the block (allocated at its first eviction, reused after)
+        and the parameters become views of it. The next load finds pinned pieces in the
+        layout and copies them back in one DMA. Returns False to take the per-parameter path.
+        """
+        layout, gpu = res_entry.param_layout, res_entry.gpu_tensor
+        if not self._has_cuda or layout is None or gpu is None or set(names) != {n for n, *_ in layout}:
+            return False
+        base = gpu.view(torch.uint8)
+        bptr = base.data_ptr()
+        end = 0
+        for name, _shape, dtype, off, numel in layout:
+            d = _get_param_data(module, name)
+            if (d.device != gpu.device or d.dtype != dtype or d.numel() != numel or not d.is_contiguous()
+                    or d.data_ptr() != bptr + off):
+                return False
+            end = max(end, off + numel * dtype.itemsize)
+        home = self._host_homes.get(block_id)
+        if home is None or home.numel() < end:
+            home = torch.empty(end, dtype=torch.uint8, pin_memory=True)
+            self._host_homes[block_id] = home
+        ev = self._engine.d2h_into(base[:end], home[:end])
+        _restore_params_from_tensor(module, home, layout)
+        if ev is not None:
+            self._d2h_fences[block_id] = ev
+        return True
 
     def _take_host_copies(self, block_id: str, module: nn.Module, names: list[str]) -> list[str]:
         """Points frozen parameters kept with a host copy back at it; returns the names still to copy back."""
@@ -385,6 +418,7 @@ class StagehandScheduler:
                     pass
         self._file_maps.clear()
         self._weight_files.close()
+        self._host_homes.clear()
         self._v2_locations.clear()
         self._squareq_layers.clear()
         self._module_param_caches.clear()
@@ -793,7 +827,11 @@ class StagehandScheduler:
         module = block_entry.module_ref()
         if module is None:
             return
-        self._sync_d2h_fences(block_id)
+        # The parameters' host tensors written by the last save-back are pinned: the loader
+        # copies them straight to the device after that copy, so the host need not wait for it.
+        d2h_fence = self._d2h_fences.pop(block_id, None) if self._has_cuda else None
+        if not self._has_cuda:
+            self._sync_d2h_fences(block_id)
         layout = _build_param_layout(module, block_entry.dtype)
         res_entry.param_layout = layout
         numel = block_entry.size_bytes // block_entry.dtype.itemsize
@@ -803,7 +841,12 @@ class StagehandScheduler:
         gpu_bytes = gpu_tensor.view(torch.uint8)
         if self._has_cuda:
             source = self._build_module_source(block_entry, module, layout)
-            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True)
+            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True,
+                                                            wait_event=d2h_fence)
+            if d2h_fence is not None and any(p.grad is not None and p.grad.device.type == "cpu"
+                                             for p in module.parameters()):
+                # saved-back gradients move to the device on the current stream, after their save-back
+                d2h_fence.wait_on(torch.cuda.current_stream().cuda_stream)
             if getattr(self._config, "frozen_host_copies", False):
                 params = dict(module.named_parameters())
                 keep = {}
@@ -898,6 +941,8 @@ class StagehandScheduler:
                 self._await_pending_load(block_id)
                 if module is not None:
                     names = self._take_host_copies(block_id, module, [n for n, _ in module.named_parameters()])
+                    if self._save_block_home(block_id, module, res_entry, names):
+                        names = []
                     self._save_params_to_host(block_id, module, names, with_grads=True)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None

@@ -68,6 +68,10 @@ class NativeEvent:
     def synchronize(self) -> None:
         _native.call("sh_event_sync", self.handle)
 
+    def wait_on(self, stream_handle: int) -> None:
+        """Makes ``stream_handle`` wait for this event on the device."""
+        _native.call("sh_stream_wait_event", stream_handle, self.handle)
+
     def __del__(self) -> None:
         try:
             if self.handle is not None:
@@ -254,12 +258,14 @@ class AsyncTransferEngine:
     # ── native block loads ───────────────────────────────────────────
 
     def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor,
-                          dest_on_loader_stream: bool = False) -> TransferHandle:
+                          dest_on_loader_stream: bool = False, wait_event: NativeEvent | None = None) -> TransferHandle:
         """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path).
 
         The copy waits for the work queued on the current stream (``gpu_dest`` may reuse
         memory that queued kernels still read) unless ``gpu_dest`` came from
-        ``alloc_device`` (``dest_on_loader_stream``)."""
+        ``alloc_device`` (``dest_on_loader_stream``). Pieces that are pinned host tensors are
+        copied straight to the device, with no slab and no host copy; ``wait_event`` (such as
+        the save-back copy that wrote them) orders every copy after it on the device."""
         if not self._has_cuda:
             raise RuntimeError("submit_block_load needs a GPU")
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
@@ -273,14 +279,37 @@ class AsyncTransferEngine:
                 pieces = [p for i, p in enumerate(source.pieces) if i in source.mutable]
         tensors = [(off, t) for off, t in pieces if isinstance(t, torch.Tensor)]
         files = [(off, t) for off, t in pieces if not isinstance(t, torch.Tensor)]
-        items = np.zeros(len(tensors), dtype=COPY_ITEM_DTYPE)
-        keep: list = [gpu_dest]
-        for i, (off, t) in enumerate(tensors):
+        for i, (_off, t) in enumerate(tensors):
             if t.device.type != "cpu" or not t.is_contiguous():
                 raise ValueError(f"block {block_id}: piece {i} must be a contiguous host tensor")
-            items[i] = (off, t.data_ptr(), t.numel() * t.element_size())
+        pinned = [t.is_pinned() for _off, t in tensors]
+        items = np.zeros(len(tensors) - sum(pinned), dtype=COPY_ITEM_DTYPE)
+        dma = np.zeros(sum(pinned), dtype=COPY_ITEM_DTYPE)
+        keep: list = [gpu_dest]
+        ni = nd = 0
+        for (off, t), pin in zip(tensors, pinned):
+            row = (off, t.data_ptr(), t.numel() * t.element_size())
+            if pin:
+                dma[nd] = row
+                nd += 1
+            else:
+                items[ni] = row
+                ni += 1
             keep.append(t)
-        keep.append(items)
+        if len(dma) > 1:
+            # pieces contiguous both in the source slab and in host memory become one copy
+            dma = np.sort(dma, order="dst")
+            merged = [dma[0].copy()]
+            for row in dma[1:]:
+                last = merged[-1]
+                if last["dst"] + last["bytes"] == row["dst"] and last["src"] + last["bytes"] == row["src"]:
+                    last["bytes"] += row["bytes"]
+                else:
+                    merged.append(row.copy())
+            dma = np.array(merged, dtype=COPY_ITEM_DTYPE)
+        keep += [items, dma]
+        if wait_event is not None:
+            keep.append(wait_event)
         ranges = np.zeros(len(files), dtype=FILE_RANGE_DTYPE)
         for i, (off, fr) in enumerate(files):
             ranges[i] = (fr.file.handle, fr.offset, fr.nbytes, off)
@@ -299,6 +328,9 @@ class AsyncTransferEngine:
         req[0]["image"] = image
         req[0]["ranges"] = ranges.ctypes.data if len(ranges) else 0
         req[0]["n_ranges"] = len(ranges)
+        req[0]["dma"] = dma.ctypes.data if len(dma) else 0
+        req[0]["n_dma"] = len(dma)
+        req[0]["wait_event"] = wait_event.handle.value if wait_event is not None else 0
         if source.plan is not None:
             if dest_on_loader_stream:
                 with torch.cuda.stream(self._loader_copy_stream()):
@@ -366,6 +398,7 @@ class AsyncTransferEngine:
         self._trace_ref.record(_current_stream_handle())
         self._trace_loads = []
         self._trace_compute = []
+        self._trace_d2h = []
 
     @property
     def tracing(self) -> bool:
@@ -386,17 +419,19 @@ class AsyncTransferEngine:
                     break
 
     def stop_trace(self) -> dict:
-        """Drains and returns {"loads": [(block, bytes, start, copied, done) ms], "compute": [(block, start, end) ms]}."""
+        """Drains and returns {"loads": [(block, bytes, start, copied, done) ms], "compute": [(block, start,
+        end) ms], "d2h": [(bytes, start, end ms, "block" | "params")] (save-back copies)}."""
         if self._trace_ref is None:
-            return {"loads": [], "compute": []}
+            return {"loads": [], "compute": [], "d2h": []}
         self.drain()
         torch.cuda.synchronize()
         ref = self._trace_ref
         compute = [(bid, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev)) for bid, s_ev, e_ev in self._trace_compute]
-        out = {"loads": list(self._trace_loads), "compute": compute}
+        d2h = [(n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind) for n, s_ev, e_ev, kind in self._trace_d2h]
+        out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h}
         _native.call("sh_loader_set_timing", self._loader_handle(), 0)
         self._trace_ref = None
-        self._trace_loads, self._trace_compute = [], []
+        self._trace_loads, self._trace_compute, self._trace_d2h = [], [], []
         return out
 
     def _record_ticket_times(self, handle: TransferHandle) -> None:
@@ -422,6 +457,10 @@ class AsyncTransferEngine:
             return [t.detach().to("cpu").clone() for t in tensors], None
         cs = self._copy_stream.cuda_stream
         self._fence_copy_stream(cs)
+        t_start = None
+        if self._trace_ref is not None:
+            t_start = NativeEvent(timing=True)
+            t_start.record(cs)
         outs, keep = [], []
         for t in tensors:
             src = t.detach()
@@ -437,9 +476,40 @@ class AsyncTransferEngine:
             keep.append(src)
         ev = NativeEvent()
         ev.record(cs)
+        if t_start is not None:
+            t_end = NativeEvent(timing=True)
+            t_end.record(cs)
+            self._trace_d2h.append((sum(k.numel() * k.element_size() for k in keep), t_start, t_end, "params"))
         with self._lock:
             self._pending_d2h.append((ev, keep))
         return outs, ev
+
+    def d2h_into(self, src: torch.Tensor, dst: torch.Tensor) -> NativeEvent | None:
+        """One copy of the contiguous device tensor ``src`` into the pinned host tensor ``dst`` on the
+        copy stream, after the work queued so far on the current stream; returns its event."""
+        nbytes = src.numel() * src.element_size()
+        if dst.numel() * dst.element_size() < nbytes or not src.is_contiguous() or not dst.is_contiguous():
+            raise ValueError("d2h_into needs contiguous tensors and a destination at least as large as the source")
+        if not self._has_cuda:
+            dst.view(torch.uint8)[:nbytes].copy_(src.reshape(-1).view(torch.uint8))
+            return None
+        cs = self._copy_stream.cuda_stream
+        self._fence_copy_stream(cs)
+        t_start = None
+        if self._trace_ref is not None:
+            t_start = NativeEvent(timing=True)
+            t_start.record(cs)
+        self._check_copy(_native.lib().sh_memcpy_d2h_async(dst.data_ptr(), src.data_ptr(), nbytes, cs), "block", "d2h")
+        self.bytes_d2h += nbytes
+        ev = NativeEvent()
+        ev.record(cs)
+        if t_start is not None:
+            t_end = NativeEvent(timing=True)
+            t_end.record(cs)
+            self._trace_d2h.append((nbytes, t_start, t_end, "block"))
+        with self._lock:
+            self._pending_d2h.append((ev, [src, dst]))
+        return ev
 
     def _reap_d2h(self, block: bool = False) -> None:
         """Drops the device references of completed save-back copies (they complete in order)."""

@@ -397,3 +397,40 @@ def test_layer_mode_fp32_matches_unwrapped(inference_mode):
                     assert torch.allclose(p.grad.to(q.grad.device), q.grad, atol=1e-5), (step, name)
     finally:
         rt.shutdown()
+
+
+def test_pinned_pieces_go_straight_to_the_device_after_their_save_back():
+    """Pinned host pieces (the outputs of a save-back copy) are copied straight to the device after
+    the save-back's event, mixed with pageable pieces that go through slabs, across several slab
+    chunks; every byte lands where its piece says."""
+    from stagehand_amd.pool import PinnedPool
+    from stagehand_amd.transfer import AsyncTransferEngine, BlockSource
+
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    a = torch.randint(0, 256, (3 << 19,), dtype=torch.uint8, device="cuda", generator=g)   # 1.5 MiB
+    b = torch.randint(0, 256, (5000,), dtype=torch.uint8, device="cuda", generator=g)
+    (ha, hb), ev = eng.d2h_async([a, b])
+    assert ha.is_pinned() and hb.is_pinned()
+    pageable = torch.randint(0, 256, ((5 << 19) + 7,), dtype=torch.uint8)                 # 2.5 MiB + 7
+    assert not pageable.is_pinned()
+    layout = [(0, ha), (ha.numel(), pageable), (ha.numel() + pageable.numel(), hb)]
+    total = sum(t.numel() for _o, t in layout)
+    dst = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    h = eng.submit_block_load("mixed", BlockSource(layout, total), dst, wait_event=ev)
+    eng.wait(h)
+    want = torch.cat([a.cpu(), pageable, b.cpu()])
+    assert torch.equal(dst.cpu(), want)
+    eng.shutdown()
+    pool.shutdown()
+    # all pinned: no slab is used at all
+    pool2 = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng2 = AsyncTransferEngine(pool2)
+    dst2 = torch.zeros(ha.numel() + hb.numel(), dtype=torch.uint8, device="cuda")
+    h = eng2.submit_block_load("pinned", BlockSource([(0, ha), (ha.numel(), hb)], dst2.numel()), dst2)
+    eng2.wait(h)
+    assert torch.equal(dst2.cpu(), torch.cat([a.cpu(), b.cpu()]))
+    assert pool2.stats()["peak_in_use"] == 0
+    eng2.shutdown()
+    pool2.shutdown()
