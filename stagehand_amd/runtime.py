@@ -199,8 +199,9 @@ class StagehandRuntime:
         if idx is None:
             return False
         handle = self._vmm.models[self._vmm_model_id]
-        handle.prefetch_block(idx + 1)
-        tensor, ok = handle.get_block_tensor(idx, torch.cuda.current_stream().cuda_stream)
+        stream = torch.cuda.current_stream().cuda_stream
+        tensor, ok = handle.get_block_tensor(idx, stream)
+        handle.prefetch_block(idx + 1, stream)  # the next block's fill runs while this one computes
         if not ok:
             return False
         try:

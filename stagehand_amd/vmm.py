@@ -248,6 +248,9 @@ class VmmModelHandle:
         self._destroyed = False
         self._files: dict[str, tuple] = {}  # path → (file object, mmap, memoryview)
         self._weight_files: dict[str, "WeightFile"] = {}  # path → native reader (file_reader != "mmap")
+        # block → (handle, tensor, load, generation, stream) of a fill started ahead by prefetch_block
+        self._pending_fills: dict[int, tuple] = {}
+        self.fills_ahead = 0  # blocks served from a fill that prefetch_block started
         self._block_pieces: list[list[tuple[int, str, int, int]]] = []  # per block: (dst off, file, file off, bytes)
         self._ram_weight_refs: list[torch.Tensor | None] = [None] * self.block_count
 
@@ -322,6 +325,21 @@ class VmmModelHandle:
         """(tensor, True), or (None, False) when the region is watermarked (vmm_backend.py:190-222)."""
         if self.block_shapes[block_idx] is None:
             raise RuntimeError(f"Block {block_idx} shape not registered. Call register_block_shape first.")
+        pending = self._pending_fills.pop(block_idx, None)
+        if pending is not None:
+            # filled ahead by prefetch_block: the caller's stream waits for that load on the device
+            p_handle, tensor, load, gen, p_stream = pending
+            if p_stream != stream:
+                # a handle's release orders eviction after its own stream: take one on the caller's
+                # (the region is held throughout, so the fill cannot be unmapped under the load)
+                own = self.allocator.ensure_resident(self.slab_id, self.regions[block_idx], stream)
+                p_handle.release()
+                p_handle = own
+            self._engine.wait_device(load, stream)
+            self._filled_generation[block_idx] = gen
+            self._active_handles[block_idx] = p_handle
+            self.fills_ahead += 1
+            return tensor, True
         handle = None
         try:
             handle = self.allocator.ensure_resident(self.slab_id, self.regions[block_idx], stream)
@@ -355,24 +373,52 @@ class VmmModelHandle:
             return [(0, ram.detach().reshape(-1).contiguous().view(torch.uint8))]
         raise RuntimeError(f"No weight source for block {block_idx}")
 
+    def _submit_fill(self, block_idx: int, vmm_tensor: torch.Tensor):
+        """Starts the load of the block's weights into its region; returns the transfer handle."""
+        from stagehand_amd.transfer import BlockSource
+
+        dst = vmm_tensor.view(-1).view(torch.uint8)
+        pieces = self._host_pieces(block_idx)
+        src_bytes = max((off + t.numel() for off, t in pieces), default=0)
+        return self._engine.submit_block_load(f"{self.model_id}:{block_idx}", BlockSource(pieces, src_bytes),
+                                              dst[:src_bytes])
+
     def _populate_block(self, block_idx: int, vmm_tensor: torch.Tensor) -> None:
         dst = vmm_tensor.view(-1).view(torch.uint8)
         pieces = self._host_pieces(block_idx)
         if self._engine is not None and torch.cuda.is_available():
-            from stagehand_amd.transfer import BlockSource
-
-            src_bytes = max((off + t.numel() for off, t in pieces), default=0)
-            handle = self._engine.submit_block_load(f"{self.model_id}:{block_idx}", BlockSource(pieces, src_bytes),
-                                                    dst[:src_bytes])
-            self._engine.wait_device(handle)
+            self._engine.wait_device(self._submit_fill(block_idx, vmm_tensor))
         else:
             for off, t in pieces:
                 dst[off:off + t.numel()].copy_(t, non_blocking=True)
 
-    def prefetch_block(self, block_idx: int) -> None:
-        """Maps the block's region ahead on the allocator's worker and warms the file pages."""
+    def prefetch_block(self, block_idx: int, stream: int | None = None) -> None:
+        """Maps the block's region ahead and warms its file pages (vmm_backend.py:283-291). With the
+        block loader and a ``stream``, a region whose contents are stale is mapped now and its fill
+        starts on the loader at once, holding the region until ``get_block_tensor`` takes it."""
         if not 0 <= block_idx < self.block_count:
             return
+        if (stream is not None and self._engine is not None and torch.cuda.is_available()
+                and self.block_shapes[block_idx] is not None and block_idx not in self._pending_fills
+                and block_idx not in self._active_handles):
+            handle = None
+            try:
+                handle = self.allocator.ensure_resident(self.slab_id, self.regions[block_idx], stream)
+                gen = handle.generation()
+                if self._filled_generation[block_idx] == gen:
+                    handle.release()  # mapped and filled already
+                    return
+                tensor = handle.as_tensor(self.dtype, self.block_shapes[block_idx])
+                load = self._submit_fill(block_idx, tensor)
+                self._pending_fills[block_idx] = (handle, tensor, load, gen, stream)
+                return
+            except MemoryError:
+                if handle is not None and not handle.released:
+                    handle.release()
+            except Exception:
+                if handle is not None and not handle.released:
+                    handle.release()
+                raise
         try:
             self.allocator.prefetch(self.slab_id, self.regions[block_idx])
         except Exception:
@@ -409,6 +455,16 @@ class VmmModelHandle:
     def release_all(self) -> None:
         for idx in list(self._active_handles):
             self.release_block(idx)
+        self._drop_pending_fills()
+
+    def _drop_pending_fills(self) -> None:
+        """Releases fills started ahead and never taken, after their loads on the device (a
+        region's release orders its eviction after the work on the handle's stream)."""
+        for _idx, (handle, _tensor, load, _gen, stream) in list(self._pending_fills.items()):
+            self._engine.wait_device(load, stream)
+            if not handle.released:
+                handle.release()
+        self._pending_fills.clear()
 
     def release_mmap(self) -> None:
         """Lets the OS drop the file's pages (they are re-read on the next fill)."""

@@ -264,6 +264,9 @@ def test_runtime_serves_blocks_from_vmm(tmp_path, mode, reader):
         assert max(g for g in handle._filled_generation if g is not None) >= 2
     assert stats["unmap_failures"] == 0
     assert not rt._vmm_active_blocks
+    if not tight:
+        assert handle.fills_ahead >= 5  # the first step filled every block after the first ahead of its use
+    assert not handle._pending_fills
     if reader == "pread":
         read = sum(f.info()["bytes_buffered"] for f in handle._weight_files.values())
         filled = sum(size for size, g in zip(handle.block_sizes, handle._filled_generation) if g is not None)
