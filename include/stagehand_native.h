@@ -327,7 +327,9 @@ typedef struct sh_load_request {
   uint64_t n_ranges;
   /* Optional pieces whose sources are pinned host memory (dst = byte offset
    * in the source, as for pieces): copied straight from their source to the
-   * device by the copy engine, with no slab and no host copy. The regions of
+   * device by the copy engine, with no slab and no host copy. Their sources
+   * are read until the load completes (not only until the ticket is issued,
+   * as for pieces): keep them alive and unchanged until then. The regions of
    * the other pieces and ranges must not overlap them. */
   const sh_copy_item* dma;
   uint64_t n_dma;

@@ -264,8 +264,10 @@ class AsyncTransferEngine:
         The copy waits for the work queued on the current stream (``gpu_dest`` may reuse
         memory that queued kernels still read) unless ``gpu_dest`` came from
         ``alloc_device`` (``dest_on_loader_stream``). Pieces that are pinned host tensors are
-        copied straight to the device, with no slab and no host copy; ``wait_event`` (such as
-        the save-back copy that wrote them) orders every copy after it on the device."""
+        copied straight to the device, with no slab and no host copy, so they are read until the
+        load completes and must not change before then (the handle keeps them alive);
+        ``wait_event`` (such as the save-back copy that wrote them) orders every copy after it on
+        the device."""
         if not self._has_cuda:
             raise RuntimeError("submit_block_load needs a GPU")
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
