@@ -842,7 +842,7 @@ class StagehandScheduler:
         if self._has_cuda:
             source = self._build_module_source(block_entry, module, layout)
             res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True,
-                                                            wait_event=d2h_fence)
+                                                            wait_event=d2h_fence, pinned_pieces=True)
             if d2h_fence is not None and any(p.grad is not None and p.grad.device.type == "cpu"
                                              for p in module.parameters()):
                 # saved-back gradients move to the device on the current stream, after their save-back

@@ -258,14 +258,17 @@ class AsyncTransferEngine:
     # ── native block loads ───────────────────────────────────────────
 
     def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor,
-                          dest_on_loader_stream: bool = False, wait_event: NativeEvent | None = None) -> TransferHandle:
+                          dest_on_loader_stream: bool = False, wait_event: NativeEvent | None = None,
+                          pinned_pieces: bool = False) -> TransferHandle:
         """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path).
 
         The copy waits for the work queued on the current stream (``gpu_dest`` may reuse
         memory that queued kernels still read) unless ``gpu_dest`` came from
-        ``alloc_device`` (``dest_on_loader_stream``). Pieces that are pinned host tensors are
-        copied straight to the device, with no slab and no host copy, so they are read until the
-        load completes and must not change before then (the handle keeps them alive);
+        ``alloc_device`` (``dest_on_loader_stream``). With ``pinned_pieces`` (or a ``wait_event``),
+        pieces that are pinned host tensors are copied straight to the device, with no slab and no
+        host copy, so they are read until the load completes and must not change before then (the
+        handle keeps them alive; asking each piece whether it is pinned costs a runtime query, so
+        callers whose pieces are never pinned leave it off);
         ``wait_event`` (such as the save-back copy that wrote them) orders every copy after it on
         the device."""
         if not self._has_cuda:
@@ -284,7 +287,8 @@ class AsyncTransferEngine:
         for i, (_off, t) in enumerate(tensors):
             if t.device.type != "cpu" or not t.is_contiguous():
                 raise ValueError(f"block {block_id}: piece {i} must be a contiguous host tensor")
-        pinned = [t.is_pinned() for _off, t in tensors]
+        check = pinned_pieces or wait_event is not None
+        pinned = [check and t.is_pinned() for _off, t in tensors]
         items = np.zeros(len(tensors) - sum(pinned), dtype=COPY_ITEM_DTYPE)
         dma = np.zeros(sum(pinned), dtype=COPY_ITEM_DTYPE)
         keep: list = [gpu_dest]

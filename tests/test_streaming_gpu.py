@@ -428,7 +428,8 @@ def test_pinned_pieces_go_straight_to_the_device_after_their_save_back():
     pool2 = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
     eng2 = AsyncTransferEngine(pool2)
     dst2 = torch.zeros(ha.numel() + hb.numel(), dtype=torch.uint8, device="cuda")
-    h = eng2.submit_block_load("pinned", BlockSource([(0, ha), (ha.numel(), hb)], dst2.numel()), dst2)
+    h = eng2.submit_block_load("pinned", BlockSource([(0, ha), (ha.numel(), hb)], dst2.numel()), dst2,
+                               pinned_pieces=True)
     eng2.wait(h)
     assert torch.equal(dst2.cpu(), torch.cat([a.cpu(), b.cpu()]))
     assert pool2.stats()["peak_in_use"] == 0
