@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 2
+#define SH_ABI_VERSION 3
 
 enum sh_status {
   SH_OK = 0,
@@ -340,6 +340,12 @@ typedef struct sh_load_request {
    * copying the dma pieces into the image. It must stay valid until the
    * ticket is issued. */
   void* wait_event;
+  /* Optional save-back ticket (sh_saveback_submit) the loader's worker waits
+   * for on the host before it issues any copy of this request, e.g. the SDMA
+   * copy that wrote the pinned sources of `dma` (no reference counterpart, as
+   * for wait_event). Do not release the ticket before the load completes. */
+  struct sh_saveback* saveback;
+  uint64_t saveback_ticket;
 } sh_load_request;
 
 typedef struct sh_loader sh_loader;
@@ -363,6 +369,40 @@ int sh_loader_release(sh_loader* loader, uint64_t ticket);
  * event recorded earlier); call it before sh_loader_release. */
 int sh_loader_set_timing(sh_loader* loader, int enable);
 int sh_loader_ticket_times(sh_loader* loader, uint64_t ticket, void* ref_event, float* out3);
+
+/* ───────────────────────── save-back copies on an SDMA engine ─────────────────────────
+ * Device-to-host copies of evicted blocks' bytes into pinned host memory (the
+ * reference copies back synchronously with `param.data.to("cpu")`,
+ * src/stagehand/scheduler.py:1216-1226 and 1348-1366), issued on a system DMA
+ * engine through the HSA runtime instead of hipMemcpyAsync, which runs a pinned
+ * device-to-host copy as a kernel on the compute units and slows the compute
+ * kernels beside it. A submit records an event on `stream`; the engine's worker
+ * thread waits for it on the host and then issues the copies, so they read what
+ * the work queued on `stream` before the submit wrote. items[i] is a (pinned
+ * host dst, device src, bytes) triple; both buffers stay in use until the ticket
+ * completes. Tickets complete in submission order: query and wait report a
+ * ticket complete only when every earlier ticket not yet released is, so a later
+ * ticket covers the copies of earlier ones. Consumers wait on the host (query,
+ * wait) or in the loader (sh_load_request.saveback). No reference counterpart. */
+typedef struct sh_saveback sh_saveback;
+int sh_saveback_create(int device, sh_saveback** out);
+/* Issues what is still queued, waits for every ticket, stops the worker and
+ * frees the engine; returns the first copy failure, if any. */
+int sh_saveback_destroy(sh_saveback* sb);
+int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream, uint64_t* ticket);
+/* SH_OK when the ticket (and every earlier one) is complete, SH_ERR_NOT_READY
+ * before, or the failure of a copy. */
+int sh_saveback_query(sh_saveback* sb, uint64_t ticket);
+int sh_saveback_wait(sh_saveback* sb, uint64_t ticket);
+/* Waits for the ticket's own copies, then forgets it (releasing twice is a no-op). */
+int sh_saveback_release(sh_saveback* sb, uint64_t ticket);
+/* Timing (telemetry): with timing on, sh_saveback_ticket_times waits for a later
+ * ticket and returns the start and end of its copies in ns of the HSA system
+ * clock, which sh_saveback_clock_ns reads (for a ticket of several copies the
+ * start is the issue of the first). Call it before releasing the ticket. */
+int sh_saveback_set_timing(sh_saveback* sb, int enable);
+int sh_saveback_clock_ns(uint64_t* ns);
+int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64_t* out2);
 
 /* ───────────────────────── turbo window engine ─────────────────────────
  * A fixed window of device slots that blocks rotate through: the HIP rewrite

@@ -157,6 +157,15 @@ _SIGNATURES: dict[str, list] = {
     "sh_loader_release": [_vp, ctypes.c_uint64],
     "sh_loader_set_timing": [_vp, _i32],
     "sh_loader_ticket_times": [_vp, ctypes.c_uint64, _vp, _vp],
+    "sh_saveback_create": [_i32, ctypes.POINTER(_vp)],
+    "sh_saveback_destroy": [_vp],
+    "sh_saveback_submit": [_vp, _vp, ctypes.c_uint64, _vp, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_query": [_vp, ctypes.c_uint64],
+    "sh_saveback_wait": [_vp, ctypes.c_uint64],
+    "sh_saveback_release": [_vp, ctypes.c_uint64],
+    "sh_saveback_set_timing": [_vp, _i32],
+    "sh_saveback_clock_ns": [ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_ticket_times": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
     "sh_turbo_create": [ctypes.POINTER(_vp)],
     "sh_turbo_destroy": [_vp],
     "sh_turbo_register_block": [_vp, _vp, _u32, ctypes.POINTER(_u32)],
@@ -203,6 +212,7 @@ LOAD_REQUEST_DTYPE = np.dtype([
     ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
     ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"), ("image", "<u8"),
     ("ranges", "<u8"), ("n_ranges", "<u8"), ("dma", "<u8"), ("n_dma", "<u8"), ("wait_event", "<u8"),
+    ("saveback", "<u8"), ("saveback_ticket", "<u8"),
 ])
 
 # Mirrors of `struct sh_file_range` / `struct sh_file_info`.
@@ -226,7 +236,7 @@ VMM_REGION_DTYPE = np.dtype([("state", "<u4"), ("refcount", "<u4"), ("offset", "
 # Mirror of `struct sh_copy_item`.
 COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -12,6 +12,8 @@ still what the budget reads.
 """
 from __future__ import annotations
 
+from typing import Callable
+
 import torch
 
 __all__ = ["BudgetManager"]
@@ -35,11 +37,21 @@ class BudgetManager:
             )
         self._high_watermark_mb = high_watermark_mb
         self._low_watermark_mb = low_watermark_mb
+        self._releasing: Callable[[], int] | None = None
+
+    def count_as_released(self, releasing_bytes: Callable[[], int] | None) -> None:
+        """Bytes ``releasing_bytes()`` returns are left out of the used figure: device memory
+        that evicted blocks gave up but that asynchronous save-back copies still hold until
+        they complete. The reference's synchronous save-back frees it before the next check."""
+        self._releasing = releasing_bytes
 
     def vram_used_mb(self) -> float:
         if not torch.cuda.is_available():
             return 0.0
-        return _allocated_bytes() / (1024 * 1024)
+        used = _allocated_bytes()
+        if self._releasing is not None:
+            used = max(0, used - int(self._releasing()))
+        return used / (1024 * 1024)
 
     def vram_reserved_mb(self) -> float:
         if not torch.cuda.is_available():

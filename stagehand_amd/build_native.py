@@ -24,6 +24,8 @@ LIB_NAME = "libstagehand_native.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 
 OFFLOAD_ARCH = "gfx950"
+# the HSA runtime (save-back copies on SDMA engines, sh_saveback.cpp)
+ROCM_LIB = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
 # No fast-math and no denormal flushing: the unpack kernels must round exactly
@@ -57,7 +59,7 @@ def build(verbose: bool = False) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = LIB_DIR / (LIB_NAME + ".tmp")
     cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}",
-           *[str(s) for s in sources()], "-o", str(tmp), "-lpthread"]
+           *[str(s) for s in sources()], "-o", str(tmp), "-lpthread", f"-L{ROCM_LIB}", "-lhsa-runtime64"]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

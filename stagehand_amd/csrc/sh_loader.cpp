@@ -65,6 +65,8 @@ struct Ticket {
   std::vector<sh_file_range> ranges;
   std::vector<sh_copy_item> dma;  // pinned sources copied straight to the device
   hipEvent_t wait_event = nullptr;
+  sh_saveback* saveback = nullptr;  // save-back ticket waited for on the host before any copy
+  uint64_t saveback_ticket = 0;
   bool advised = false;
   uint64_t src_bytes = 0;
   const sh_plan* plan = nullptr;
@@ -156,6 +158,14 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   // after the copy. A block may therefore be larger than one slab; with two
   // or more slabs the gather of chunk k+1 overlaps the H2D of chunk k.
   void* h2d_dst = t.plan ? t.staging : t.dst;
+  if (t.saveback != nullptr) {
+    // the save-back that wrote pinned sources of this load runs on an SDMA engine: wait on the host
+    int st = sh_saveback_wait(t.saveback, t.saveback_ticket);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      return st;
+    }
+  }
   e = hipStreamWaitEvent(L->copy_stream, t.ready, 0);
   if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(ready)");
   if (t.wait_event != nullptr) {
@@ -355,6 +365,7 @@ void worker_loop(sh_loader* L) {
       t->dma.clear();
       t->dma.shrink_to_fit();
       t->wait_event = nullptr;
+      t->saveback = nullptr;
     }
     L->issued_cv.notify_all();
   }
@@ -528,6 +539,8 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   if (req->n_ranges > 0) t.ranges.assign(req->ranges, req->ranges + req->n_ranges);
   if (req->n_dma > 0) t.dma.assign(req->dma, req->dma + req->n_dma);
   t.wait_event = (hipEvent_t)req->wait_event;
+  t.saveback = req->saveback;
+  t.saveback_ticket = req->saveback_ticket;
   t.src_bytes = req->src_bytes;
   t.plan = req->plan;
   t.staging = req->staging;

@@ -1,0 +1,344 @@
+// Save-back copies (device -> pinned host) on a system DMA (SDMA) engine.
+//
+// Eviction with save-back copies a block's device bytes into host memory (the
+// reference's `param.data.to("cpu")`, src/stagehand/scheduler.py:1216-1226 and
+// 1348-1366). hipMemcpyAsync runs a pinned device-to-host copy as a kernel on
+// the compute units; on MI355X the compute kernels that ran beside those copies
+// in a streamed training step took many times their usual duration (a 740 MB
+// block copy overlapping a GEMM, attention or elementwise kernel; a copy
+// kernel limited to 16 workgroups still did it, a CU-masked copy stream
+// helped little). The SDMA engines copy without the compute units, so the
+// copies here go through the HSA runtime's hsa_amd_memory_async_copy, which
+// uses them for transfers between a GPU agent and the CPU agent.
+//
+// Ordering: an HSA copy cannot wait for a HIP event on the device, so each
+// submit records an event on the caller's stream and a worker thread waits
+// for it on the host before it issues the copies. Completion is an HSA signal
+// (initialised to the number of copies; each finished copy decrements it).
+// Tickets complete in submission order: query and wait report a ticket done
+// only when every live earlier ticket is, so a later ticket covers earlier
+// copies as a later event on one stream would.
+
+#include <hip/hip_runtime.h>
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
+
+#include <condition_variable>
+#include <cstdint>
+#include <deque>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "sh_internal.h"
+#include "stagehand_native.h"
+
+namespace {
+
+struct Job {
+  uint64_t id = 0;
+  hipEvent_t fence = nullptr;
+  std::vector<sh_copy_item> items;
+  hsa_signal_t done{0};
+  int status = SH_OK;  // set (under the engine lock) before a failure completes `done`
+  std::string error;
+  uint64_t issue_ticks = 0;  // HSA system clock when the worker issued the first copy (timing only)
+};
+
+hsa_status_t find_cpu(hsa_agent_t agent, void* data) {
+  hsa_device_type_t type;
+  if (hsa_agent_get_info(agent, HSA_AGENT_INFO_DEVICE, &type) == HSA_STATUS_SUCCESS && type == HSA_DEVICE_TYPE_CPU) {
+    *(hsa_agent_t*)data = agent;
+    return HSA_STATUS_INFO_BREAK;
+  }
+  return HSA_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+struct sh_saveback {
+  int device = 0;
+  hsa_agent_t cpu{0}, gpu{0};
+  std::mutex mu;
+  std::condition_variable cv;
+  std::deque<std::shared_ptr<Job>> queue;          // submitted, not yet issued by the worker
+  std::map<uint64_t, std::shared_ptr<Job>> jobs;   // every live ticket, in submission order
+  uint64_t next_id = 1;
+  bool stop = false;
+  bool timing = false;
+  std::thread worker;
+};
+
+namespace {
+
+// Records a failure, then completes the job's signal (waiters read the status after the signal).
+void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, hsa_signal_value_t outstanding) {
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    j.status = status;
+    j.error = what;
+  }
+  hsa_signal_subtract_screlease(j.done, outstanding);
+}
+
+void worker_loop(sh_saveback* sb) {
+  (void)hipSetDevice(sb->device);
+  for (;;) {
+    std::shared_ptr<Job> j;
+    {
+      std::unique_lock<std::mutex> lk(sb->mu);
+      sb->cv.wait(lk, [&] { return sb->stop || !sb->queue.empty(); });
+      if (sb->queue.empty()) return;  // stop requested and nothing left to issue
+      j = sb->queue.front();
+      sb->queue.pop_front();
+    }
+    const hsa_signal_value_t n = (hsa_signal_value_t)j->items.size();
+    hipError_t e = hipEventSynchronize(j->fence);
+    if (e != hipSuccess) {
+      fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), n);
+      continue;
+    }
+    if (sb->timing) hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &j->issue_ticks);
+    hsa_signal_value_t issued = 0;
+    for (const sh_copy_item& it : j->items) {
+      hsa_status_t s = hsa_amd_memory_async_copy(it.dst, sb->cpu, it.src, sb->gpu, it.bytes, 0, nullptr, j->done);
+      if (s != HSA_STATUS_SUCCESS) {
+        const char* msg = nullptr;
+        hsa_status_string(s, &msg);
+        // the copies already issued still decrement the signal themselves
+        fail_job(sb, *j, SH_ERR_HIP, std::string("hsa_amd_memory_async_copy: ") + (msg ? msg : "error"), n - issued);
+        break;
+      }
+      ++issued;
+    }
+  }
+}
+
+// Waits for `j` alone; SH_OK or its failure (recorded in the last error).
+int wait_job(sh_saveback* sb, const std::shared_ptr<Job>& j) {
+  hsa_signal_value_t v;
+  while ((v = hsa_signal_wait_scacquire(j->done, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, HSA_WAIT_STATE_BLOCKED)) >= 1) {
+  }
+  std::lock_guard<std::mutex> lk(sb->mu);
+  if (j->status != SH_OK) return sh::fail(j->status, "save-back ticket %llu: %s", (unsigned long long)j->id, j->error.c_str());
+  if (v < 0) return sh::fail(SH_ERR_HIP, "save-back ticket %llu: the copy engine reported an error", (unsigned long long)j->id);
+  return SH_OK;
+}
+
+// The live jobs up to and including `ticket` (in order); SH_ERR_INVALID for a ticket never issued.
+int jobs_upto(sh_saveback* sb, uint64_t ticket, std::vector<std::shared_ptr<Job>>& out, const char* who) {
+  std::lock_guard<std::mutex> lk(sb->mu);
+  if (ticket == 0 || ticket >= sb->next_id) return sh::fail(SH_ERR_INVALID, "%s: unknown ticket %llu", who, (unsigned long long)ticket);
+  for (auto it = sb->jobs.begin(); it != sb->jobs.end() && it->first <= ticket; ++it) out.push_back(it->second);
+  return SH_OK;
+}
+
+void destroy_job(Job& j) {
+  if (j.done.handle != 0) hsa_signal_destroy(j.done);
+  if (j.fence != nullptr) (void)hipEventDestroy(j.fence);
+}
+
+}  // namespace
+
+extern "C" int sh_saveback_create(int device, sh_saveback** out) {
+  sh::clear_error();
+  if (out == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_create: out is NULL");
+  *out = nullptr;
+  SH_HIP(hipSetDevice(device));
+  if (hsa_init() != HSA_STATUS_SUCCESS) return sh::fail(SH_ERR_HIP, "sh_saveback_create: hsa_init failed");
+  auto sb = std::make_unique<sh_saveback>();
+  sb->device = device;
+  // the device's HSA agent: the owner of a small allocation made on it
+  void* probe = nullptr;
+  hipError_t e = hipMalloc(&probe, 256);
+  if (e != hipSuccess) {
+    hsa_shut_down();
+    return sh::fail(SH_ERR_HIP, "sh_saveback_create: hipMalloc: %s", hipGetErrorString(e));
+  }
+  hsa_amd_pointer_info_t info{};
+  info.size = sizeof(info);
+  hsa_status_t s = hsa_amd_pointer_info(probe, &info, nullptr, nullptr, nullptr);
+  (void)hipFree(probe);
+  if (s != HSA_STATUS_SUCCESS || info.type == HSA_EXT_POINTER_TYPE_UNKNOWN || info.agentOwner.handle == 0) {
+    hsa_shut_down();
+    return sh::fail(SH_ERR_HIP, "sh_saveback_create: no HSA agent owns device %d's memory", device);
+  }
+  sb->gpu = info.agentOwner;
+  if (hsa_agent_get_info(sb->gpu, (hsa_agent_info_t)HSA_AMD_AGENT_INFO_NEAREST_CPU, &sb->cpu) != HSA_STATUS_SUCCESS ||
+      sb->cpu.handle == 0) {
+    sb->cpu.handle = 0;
+    hsa_iterate_agents(find_cpu, &sb->cpu);
+  }
+  if (sb->cpu.handle == 0) {
+    hsa_shut_down();
+    return sh::fail(SH_ERR_HIP, "sh_saveback_create: no CPU agent");
+  }
+  sh_saveback* raw = sb.release();
+  raw->worker = std::thread(worker_loop, raw);
+  *out = raw;
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_destroy(sh_saveback* sb) {
+  sh::clear_error();
+  if (sb == nullptr) return SH_OK;
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    sb->stop = true;
+  }
+  sb->cv.notify_all();
+  if (sb->worker.joinable()) sb->worker.join();  // issues everything still queued first
+  int first = SH_OK;
+  for (auto& kv : sb->jobs) {
+    int st = wait_job(sb, kv.second);
+    if (first == SH_OK) first = st;
+    destroy_job(*kv.second);
+  }
+  sb->jobs.clear();
+  delete sb;
+  hsa_shut_down();
+  return first;
+}
+
+extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream,
+                                  uint64_t* ticket) {
+  sh::clear_error();
+  if (sb == nullptr || ticket == nullptr || (n > 0 && items == nullptr))
+    return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: NULL argument");
+  *ticket = 0;
+  auto j = std::make_shared<Job>();
+  for (uint64_t i = 0; i < n; ++i) {
+    if (items[i].bytes == 0) continue;
+    if (items[i].dst == nullptr || items[i].src == nullptr)
+      return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: item %llu has a NULL pointer", (unsigned long long)i);
+    j->items.push_back(items[i]);
+  }
+  if (hsa_signal_create((hsa_signal_value_t)j->items.size(), 0, nullptr, &j->done) != HSA_STATUS_SUCCESS)
+    return sh::fail(SH_ERR_HIP, "sh_saveback_submit: hsa_signal_create failed");
+  hipError_t e = hipEventCreateWithFlags(&j->fence, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(j->fence, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    destroy_job(*j);
+    return sh::fail(SH_ERR_HIP, "sh_saveback_submit: fence event: %s", hipGetErrorString(e));
+  }
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    if (sb->stop) {
+      destroy_job(*j);
+      return sh::fail(SH_ERR_STATE, "sh_saveback_submit: the engine is being destroyed");
+    }
+    j->id = sb->next_id++;
+    sb->jobs[j->id] = j;
+    sb->queue.push_back(j);
+  }
+  sb->cv.notify_one();
+  *ticket = j->id;
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_query(sh_saveback* sb, uint64_t ticket) {
+  sh::clear_error();
+  if (sb == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_query: NULL engine");
+  std::vector<std::shared_ptr<Job>> js;
+  int st = jobs_upto(sb, ticket, js, "sh_saveback_query");
+  if (st != SH_OK) return st;
+  for (const auto& j : js) {
+    if (hsa_signal_load_scacquire(j->done) >= 1) return SH_ERR_NOT_READY;
+    st = wait_job(sb, j);  // already at its final value: returns at once
+    if (st != SH_OK) return st;
+  }
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_wait(sh_saveback* sb, uint64_t ticket) {
+  sh::clear_error();
+  if (sb == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_wait: NULL engine");
+  std::vector<std::shared_ptr<Job>> js;
+  int st = jobs_upto(sb, ticket, js, "sh_saveback_wait");
+  if (st != SH_OK) return st;
+  for (const auto& j : js) {
+    st = wait_job(sb, j);
+    if (st != SH_OK) return st;
+  }
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_release(sh_saveback* sb, uint64_t ticket) {
+  sh::clear_error();
+  if (sb == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_release: NULL engine");
+  std::shared_ptr<Job> j;
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    auto it = sb->jobs.find(ticket);
+    if (it == sb->jobs.end()) {
+      if (ticket == 0 || ticket >= sb->next_id)
+        return sh::fail(SH_ERR_INVALID, "sh_saveback_release: unknown ticket %llu", (unsigned long long)ticket);
+      return SH_OK;  // released before
+    }
+    j = it->second;
+  }
+  int st = wait_job(sb, j);  // its own copies only: they read and write the caller's buffers
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    sb->jobs.erase(ticket);
+  }
+  destroy_job(*j);
+  return st;
+}
+
+namespace {
+uint64_t ticks_to_ns(uint64_t ticks) {
+  static uint64_t freq = 0;
+  if (freq == 0 && hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) != HSA_STATUS_SUCCESS) freq = 0;
+  if (freq == 0) return 0;
+  return (uint64_t)((__uint128_t)ticks * 1000000000ull / freq);
+}
+}  // namespace
+
+extern "C" int sh_saveback_set_timing(sh_saveback* sb, int enable) {
+  sh::clear_error();
+  if (sb == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_set_timing: NULL engine");
+  // the runtime-wide switch stays on once set: the HIP runtime's own copies may rely on it
+  if (enable && hsa_amd_profiling_async_copy_enable(true) != HSA_STATUS_SUCCESS)
+    return sh::fail(SH_ERR_HIP, "sh_saveback_set_timing: hsa_amd_profiling_async_copy_enable failed");
+  std::lock_guard<std::mutex> lk(sb->mu);
+  sb->timing = enable != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_clock_ns(uint64_t* ns) {
+  sh::clear_error();
+  if (ns == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_clock_ns: NULL argument");
+  uint64_t t = 0;
+  if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &t) != HSA_STATUS_SUCCESS)
+    return sh::fail(SH_ERR_HIP, "sh_saveback_clock_ns: hsa_system_get_info failed");
+  *ns = ticks_to_ns(t);
+  return SH_OK;
+}
+
+extern "C" int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64_t* out2) {
+  sh::clear_error();
+  if (sb == nullptr || out2 == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_ticket_times: NULL argument");
+  std::shared_ptr<Job> j;
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    auto it = sb->jobs.find(ticket);
+    if (it == sb->jobs.end()) return sh::fail(SH_ERR_INVALID, "sh_saveback_ticket_times: unknown or released ticket");
+    j = it->second;
+  }
+  int st = wait_job(sb, j);
+  if (st != SH_OK) return st;
+  out2[0] = out2[1] = 0;
+  if (j->items.empty()) return SH_OK;
+  hsa_amd_profiling_async_copy_time_t t{};
+  if (hsa_amd_profiling_get_async_copy_time(j->done, &t) != HSA_STATUS_SUCCESS || t.end == 0)
+    return sh::fail(SH_ERR_STATE, "sh_saveback_ticket_times: the ticket was submitted without timing");
+  // the signal holds the last copy's times; a ticket of several copies starts no later than its first issue
+  uint64_t start = t.start;
+  if (j->items.size() > 1 && j->issue_ticks != 0 && j->issue_ticks < start) start = j->issue_ticks;
+  out2[0] = ticks_to_ns(start);
+  out2[1] = ticks_to_ns(t.end);
+  return SH_OK;
+}

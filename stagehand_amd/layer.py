@@ -125,7 +125,8 @@ class LayerRuntime:
         self._config.telemetry_enabled = telemetry
         self._pool = pool if pool is not None else PinnedPool(total_mb=self._config.pinned_pool_mb,
                                                               slab_mb=self._config.pinned_slab_mb)
-        self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=self._config.max_inflight_transfers)
+        self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=self._config.max_inflight_transfers,
+                                           save_back=self._config.save_back_engine)
         self._budget = BudgetManager(self._config.vram_high_watermark_mb, self._config.vram_low_watermark_mb)
         self._guards: NumericGuard | None = None
         self._telemetry_inst = StagehandTelemetry(enabled=self._config.telemetry_enabled,

@@ -75,7 +75,8 @@ class StagehandRuntime:
         self._telemetry = StagehandTelemetry(enabled=config.telemetry_enabled, interval_steps=config.telemetry_interval_steps,
                                              output_file=config.telemetry_file if config.telemetry_enabled else None)
         self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=config.max_inflight_transfers,
-                                           pin_sources=config.pinned_source_cache)
+                                           pin_sources=config.pinned_source_cache,
+                                           save_back=config.save_back_engine)
         self._scheduler = StagehandScheduler(
             registry=self._registry, residency=self._residency, transfer_engine=self._engine, budget=self._budget,
             policy=StaticLookaheadPolicy(prefetch_window=config.prefetch_window_blocks,

@@ -221,6 +221,12 @@ class StagehandScheduler:
         self._host_homes: dict[str, torch.Tensor] = {}
         # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
         self._done_marks: collections.deque = collections.deque()
+        # device memory that an eviction gave up is left out of the budget while the
+        # save-back copy still holds it (the reference's synchronous copy frees it at once)
+        count_as_released = getattr(budget, "count_as_released", None)
+        releasing = getattr(transfer_engine, "releasing_bytes", None)
+        if callable(count_as_released) and callable(releasing):
+            count_as_released(releasing)
 
     # ── step lifecycle ───────────────────────────────────────────────
 
@@ -325,6 +331,15 @@ class StagehandScheduler:
         if ev is not None:
             self._d2h_fences[block_id] = ev
         return True
+
+    def _release_with_save_back(self, block_id: str, res_entry: ResidencyEntry, fence_before: Any) -> None:
+        """The block's device buffer, about to be dropped, stays held by the save-back copy just
+        queued for it (its fence changed): count it as released for the budget from now on."""
+        fence = self._d2h_fences.get(block_id)
+        gpu = res_entry.gpu_tensor
+        if fence is None or fence is fence_before or gpu is None or not hasattr(self._engine, "release_with_copy"):
+            return
+        self._engine.release_with_copy(fence, gpu.untyped_storage().nbytes())
 
     def _take_host_copies(self, block_id: str, module: nn.Module, names: list[str]) -> list[str]:
         """Points frozen parameters kept with a host copy back at it; returns the names still to copy back."""
@@ -939,11 +954,13 @@ class StagehandScheduler:
             if module_backed:
                 self._residency.transition(block_id, BlockState.EVICTING)
                 self._await_pending_load(block_id)
+                fence_before = self._d2h_fences.get(block_id)
                 if module is not None:
                     names = self._take_host_copies(block_id, module, [n for n, _ in module.named_parameters()])
                     if self._save_block_home(block_id, module, res_entry, names):
                         names = []
                     self._save_params_to_host(block_id, module, names, with_grads=True)
+                self._release_with_save_back(block_id, res_entry, fence_before)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -954,6 +971,7 @@ class StagehandScheduler:
                 mutable = set(block_entry.module_param_names)
                 keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
                 specs = {s.param_name: s for s in block_entry.file_param_specs}
+                fence_before = self._d2h_fences.get(block_id)
                 if module is not None and res_entry.param_layout is not None:
                     to_host = []
                     for name, _shape, dtype, _off, _numel in res_entry.param_layout:
@@ -974,6 +992,7 @@ class StagehandScheduler:
                     for name, param in module.named_parameters():
                         if name in mutable and param.grad is not None and param.grad.device.type != "cpu":
                             param.grad = param.grad.to("cpu", non_blocking=True)
+                self._release_with_save_back(block_id, res_entry, fence_before)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -1003,6 +1022,7 @@ class StagehandScheduler:
 
         # No save-back: GPU_READY → GPU_FREEING → UNLOADED.
         self._residency.transition(block_id, BlockState.GPU_FREEING)
+        fence_before = self._d2h_fences.get(block_id)
         if module is not None and res_entry.param_layout is not None:
             if module_backed:
                 self._await_pending_load(block_id)
@@ -1023,6 +1043,7 @@ class StagehandScheduler:
                 self._save_params_to_host(block_id, module, to_host)
             else:
                 _detach_params(module, res_entry.param_layout)
+        self._release_with_save_back(block_id, res_entry, fence_before)
         self._release_device_buffer(res_entry)
         res_entry.param_layout = None
         self._residency.transition(block_id, BlockState.UNLOADED)

@@ -21,11 +21,13 @@ submission, as in the reference (src/stagehand/transfer.py:136-138).
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import logging
 import os
 import threading
 import time
+import weakref
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any
 
@@ -40,7 +42,7 @@ if TYPE_CHECKING:
     from stagehand_amd.pool import PinnedPool, PinnedSlab
     from stagehand_amd.unpack import UnpackPlan
 
-__all__ = ["TransferHandle", "AsyncTransferEngine", "NativeEvent", "BlockSource"]
+__all__ = ["TransferHandle", "AsyncTransferEngine", "NativeEvent", "BlockSource", "SaveBackEngine", "SaveBackTicket"]
 
 log = logging.getLogger(__name__)
 _STALL_LOGS_ENABLED = str(os.getenv("SERENITY_STAGEHAND_STALL_LOGS", "0")).strip().lower() in {"1", "true", "yes", "on"}
@@ -77,6 +79,116 @@ class NativeEvent:
             if self.handle is not None:
                 _native.lib().sh_event_destroy(self.handle)
                 self.handle = None
+        except Exception:
+            pass
+
+
+class SaveBackEngine:
+    """Device→host save-back copies on an SDMA engine (native ``sh_saveback``).
+
+    The reference copies an evicted block's parameters back with a synchronous
+    ``param.data.to("cpu")`` (src/stagehand/scheduler.py:1216-1226, 1348-1366).
+    ``hipMemcpyAsync`` would run these pinned device→host copies as kernels on
+    the compute units, which slows the compute kernels running beside them; the
+    SDMA engines copy without them. Each submission is ordered after the work
+    queued on a stream (a worker thread waits for an event recorded there) and
+    completes as a :class:`SaveBackTicket`; tickets complete in order.
+    """
+
+    def __init__(self, device: int) -> None:
+        h = ctypes.c_void_p()
+        _native.call("sh_saveback_create", int(device), ctypes.byref(h))
+        self._h: ctypes.c_void_p | None = h
+        self._timing = False
+        _LIVE_SAVEBACKS.add(self)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise RuntimeError("the save-back engine has been shut down")
+        return self._h
+
+    @property
+    def closed(self) -> bool:
+        return self._h is None
+
+    def submit(self, items: np.ndarray, stream_handle: int) -> "SaveBackTicket":
+        """Copies ``items`` (COPY_ITEM_DTYPE rows: pinned host dst, device src, bytes) after the
+        work queued so far on ``stream_handle``."""
+        ticket = ctypes.c_uint64()
+        _native.call("sh_saveback_submit", self.handle, items.ctypes.data if len(items) else None, len(items),
+                     stream_handle, ctypes.byref(ticket))
+        return SaveBackTicket(self, ticket.value)
+
+    def set_timing(self, enable: bool) -> None:
+        _native.call("sh_saveback_set_timing", self.handle, int(enable))
+        self._timing = bool(enable)
+
+    @staticmethod
+    def clock_ns() -> int:
+        ns = ctypes.c_uint64()
+        _native.call("sh_saveback_clock_ns", ctypes.byref(ns))
+        return ns.value
+
+    def close(self) -> None:
+        if self._h is not None:
+            h, self._h = self._h, None
+            _LIVE_SAVEBACKS.discard(self)
+            _native.call("sh_saveback_destroy", h)
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# Engines still open at interpreter exit are closed before the HIP runtime goes away
+# (their worker thread waits for HIP events).
+_LIVE_SAVEBACKS: "weakref.WeakSet[SaveBackEngine]" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_savebacks() -> None:
+    for sb in list(_LIVE_SAVEBACKS):
+        try:
+            sb.close()
+        except Exception:
+            pass
+
+
+class SaveBackTicket:
+    """Completion of one :class:`SaveBackEngine` submission, with the ``query`` /
+    ``synchronize`` face of :class:`NativeEvent`. It has no device-side form:
+    ``wait_on`` waits on the host, and a load that reads what it wrote passes it as
+    ``submit_block_load(wait_event=...)``, which the loader's worker waits for."""
+
+    def __init__(self, engine: SaveBackEngine, ticket: int) -> None:
+        self.engine = engine
+        self.ticket = ticket
+
+    def query(self) -> bool:
+        if self.engine.closed:  # closing the engine waited for every copy
+            return True
+        return _native.call("sh_saveback_query", self.engine.handle, self.ticket) == _native.SH_OK
+
+    def synchronize(self) -> None:
+        if not self.engine.closed:
+            _native.call("sh_saveback_wait", self.engine.handle, self.ticket)
+
+    def wait_on(self, stream_handle: int) -> None:
+        """Waits on the host (the copy engine's completion has no device-side wait)."""
+        self.synchronize()
+
+    def times_ns(self) -> tuple[int, int]:
+        out = (ctypes.c_uint64 * 2)()
+        _native.call("sh_saveback_ticket_times", self.engine.handle, self.ticket, out)
+        return out[0], out[1]
+
+    def __del__(self) -> None:
+        try:
+            if not self.engine.closed:
+                _native.lib().sh_saveback_release(self.engine.handle, ctypes.c_uint64(self.ticket))
         except Exception:
             pass
 
@@ -129,6 +241,7 @@ class AsyncTransferEngine:
         copy_stream: torch.cuda.Stream | None = None,
         copy_threads: int | None = None,
         pin_sources: bool = False,
+        save_back: str = "sdma",
     ) -> None:
         self._pool = pool
         # pin_sources: keep one pinned host image per cacheable block source and
@@ -152,7 +265,16 @@ class AsyncTransferEngine:
         self.bytes_h2d = 0
         self.bytes_d2h = 0
         self.loads = 0
-        self._pending_d2h: list[tuple[NativeEvent, list]] = []
+        # save-back copies in flight: (completion event, device/host tensors they read or
+        # write, device bytes their caller gave up with them)
+        self._pending_d2h: list[tuple[Any, list, int]] = []
+        self._releasing_bytes = 0
+        # where save-back copies run: "sdma" (SaveBackEngine) or "stream" (the copy stream)
+        if save_back not in ("sdma", "stream"):
+            raise ValueError(f"save_back must be 'sdma' or 'stream', got {save_back!r}")
+        self._save_back = save_back
+        self._saveback: SaveBackEngine | None = None
+        self._trace_t0_ns = 0
         # optional device timeline (start_trace / stop_trace)
         self._trace_ref: NativeEvent | None = None
         self._trace_loads: list[tuple[str, int, float, float, float]] = []
@@ -258,7 +380,7 @@ class AsyncTransferEngine:
     # ── native block loads ───────────────────────────────────────────
 
     def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor,
-                          dest_on_loader_stream: bool = False, wait_event: NativeEvent | None = None,
+                          dest_on_loader_stream: bool = False, wait_event: "NativeEvent | SaveBackTicket | None" = None,
                           pinned_pieces: bool = False) -> TransferHandle:
         """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path).
 
@@ -269,8 +391,9 @@ class AsyncTransferEngine:
         host copy, so they are read until the load completes and must not change before then (the
         handle keeps them alive; asking each piece whether it is pinned costs a runtime query, so
         callers whose pieces are never pinned leave it off);
-        ``wait_event`` (such as the save-back copy that wrote them) orders every copy after it on
-        the device."""
+        ``wait_event`` (such as the save-back copy that wrote them) orders every copy after it: on
+        the device for a :class:`NativeEvent`, on the loader's worker thread for a
+        :class:`SaveBackTicket`."""
         if not self._has_cuda:
             raise RuntimeError("submit_block_load needs a GPU")
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
@@ -336,7 +459,11 @@ class AsyncTransferEngine:
         req[0]["n_ranges"] = len(ranges)
         req[0]["dma"] = dma.ctypes.data if len(dma) else 0
         req[0]["n_dma"] = len(dma)
-        req[0]["wait_event"] = wait_event.handle.value if wait_event is not None else 0
+        if isinstance(wait_event, SaveBackTicket):
+            req[0]["saveback"] = wait_event.engine.handle.value
+            req[0]["saveback_ticket"] = wait_event.ticket
+        elif wait_event is not None:
+            req[0]["wait_event"] = wait_event.handle.value
         if source.plan is not None:
             if dest_on_loader_stream:
                 with torch.cuda.stream(self._loader_copy_stream()):
@@ -400,8 +527,15 @@ class AsyncTransferEngine:
         if not self._has_cuda:
             return
         _native.call("sh_loader_set_timing", self._loader_handle(), 1)
+        sb = self._saveback_engine()
+        if sb is not None:
+            sb.set_timing(True)
         self._trace_ref = NativeEvent(timing=True)
         self._trace_ref.record(_current_stream_handle())
+        if sb is not None:
+            # copy-engine times are read on the HSA system clock: take its value when the reference completes
+            self._trace_ref.synchronize()
+            self._trace_t0_ns = sb.clock_ns()
         self._trace_loads = []
         self._trace_compute = []
         self._trace_d2h = []
@@ -433,9 +567,17 @@ class AsyncTransferEngine:
         torch.cuda.synchronize()
         ref = self._trace_ref
         compute = [(bid, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev)) for bid, s_ev, e_ev in self._trace_compute]
-        d2h = [(n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind) for n, s_ev, e_ev, kind in self._trace_d2h]
+        d2h = []
+        for n, s_ev, e_ev, kind in self._trace_d2h:
+            if isinstance(s_ev, SaveBackTicket):  # copy-engine times, aligned at start_trace
+                t0, t1 = s_ev.times_ns()
+                d2h.append((n, (t0 - self._trace_t0_ns) / 1e6, (t1 - self._trace_t0_ns) / 1e6, kind))
+            else:
+                d2h.append((n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind))
         out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h}
         _native.call("sh_loader_set_timing", self._loader_handle(), 0)
+        if self._saveback is not None:
+            self._saveback.set_timing(False)
         self._trace_ref = None
         self._trace_loads, self._trace_compute, self._trace_d2h = [], [], []
         return out
@@ -450,24 +592,18 @@ class AsyncTransferEngine:
 
     # ── asynchronous parameter save-back ─────────────────────────────
 
-    def d2h_async(self, tensors: list[torch.Tensor]) -> tuple[list[torch.Tensor], NativeEvent | None]:
-        """Copies device tensors into new pinned host tensors on the copy stream.
+    def d2h_async(self, tensors: list[torch.Tensor]) -> tuple[list[torch.Tensor], "NativeEvent | SaveBackTicket | None"]:
+        """Copies device tensors into new pinned host tensors (a save-back).
 
-        Returns the host tensors and the event that marks their completion (None
-        without a GPU, where the copies are synchronous). The device tensors are
-        kept alive until the copies complete (``reap``/``drain``), so the caller
-        may drop its references at once. Ordering: the copies start after the
-        work queued so far on the current stream.
+        Returns the host tensors and what marks their completion (None without a
+        GPU, where the copies are synchronous). The device tensors are kept alive
+        until the copies complete (``reap``/``drain``), so the caller may drop its
+        references at once. Ordering: the copies start after the work queued so
+        far on the current stream.
         """
         if not self._has_cuda:
             return [t.detach().to("cpu").clone() for t in tensors], None
-        cs = self._copy_stream.cuda_stream
-        self._fence_copy_stream(cs)
-        t_start = None
-        if self._trace_ref is not None:
-            t_start = NativeEvent(timing=True)
-            t_start.record(cs)
-        outs, keep = [], []
+        outs, pairs = [], []
         for t in tensors:
             src = t.detach()
             if src.device.type == "cpu":
@@ -475,47 +611,96 @@ class AsyncTransferEngine:
                 continue
             src = src.contiguous()
             out = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
-            nbytes = src.numel() * src.element_size()
-            self._check_copy(_native.lib().sh_memcpy_d2h_async(out.data_ptr(), src.data_ptr(), nbytes, cs), "params", "d2h")
-            self.bytes_d2h += nbytes
             outs.append(out)
-            keep.append(src)
-        ev = NativeEvent()
-        ev.record(cs)
-        if t_start is not None:
-            t_end = NativeEvent(timing=True)
-            t_end.record(cs)
-            self._trace_d2h.append((sum(k.numel() * k.element_size() for k in keep), t_start, t_end, "params"))
-        with self._lock:
-            self._pending_d2h.append((ev, keep))
-        return outs, ev
+            pairs.append((out, src))
+        return outs, self._issue_save_back(pairs, "params")
 
-    def d2h_into(self, src: torch.Tensor, dst: torch.Tensor) -> NativeEvent | None:
-        """One copy of the contiguous device tensor ``src`` into the pinned host tensor ``dst`` on the
-        copy stream, after the work queued so far on the current stream; returns its event."""
+    def d2h_into(self, src: torch.Tensor, dst: torch.Tensor) -> "NativeEvent | SaveBackTicket | None":
+        """One save-back copy of the contiguous device tensor ``src`` into the pinned host tensor
+        ``dst``, after the work queued so far on the current stream; returns its completion."""
         nbytes = src.numel() * src.element_size()
         if dst.numel() * dst.element_size() < nbytes or not src.is_contiguous() or not dst.is_contiguous():
             raise ValueError("d2h_into needs contiguous tensors and a destination at least as large as the source")
         if not self._has_cuda:
             dst.view(torch.uint8)[:nbytes].copy_(src.reshape(-1).view(torch.uint8))
             return None
-        cs = self._copy_stream.cuda_stream
-        self._fence_copy_stream(cs)
-        t_start = None
-        if self._trace_ref is not None:
-            t_start = NativeEvent(timing=True)
-            t_start.record(cs)
-        self._check_copy(_native.lib().sh_memcpy_d2h_async(dst.data_ptr(), src.data_ptr(), nbytes, cs), "block", "d2h")
+        return self._issue_save_back([(dst, src)], "block")
+
+    def _saveback_engine(self) -> SaveBackEngine | None:
+        """The SDMA save-back engine (created on first use), or None when save-backs use the copy stream."""
+        if not self._has_cuda or self._save_back != "sdma":
+            return None
+        if self._saveback is None:
+            try:
+                self._saveback = SaveBackEngine(torch.cuda.current_device())
+            except Exception as exc:  # noqa: BLE001 — the copy stream is the other device path
+                log.warning("AsyncTransferEngine: no SDMA save-back engine (%s); save-backs use the copy stream", exc)
+                self._save_back = "stream"
+                return None
+        return self._saveback
+
+    def _issue_save_back(self, pairs: list[tuple[torch.Tensor, torch.Tensor]],
+                         kind: str) -> "NativeEvent | SaveBackTicket":
+        """Copies each (pinned host dst, device src) pair after the work queued so far on the current
+        stream: on the SDMA engine when there is one (one ticket), else on the copy stream (one
+        event). Either way, completions are in submission order, and the pending list keeps the
+        tensors alive until theirs."""
+        nbytes = sum(src.numel() * src.element_size() for _dst, src in pairs)
+        keep = [t for pair in pairs for t in pair]
+        sb = self._saveback_engine()
+        done: NativeEvent | SaveBackTicket
+        if sb is not None:
+            items = np.zeros(len(pairs), dtype=COPY_ITEM_DTYPE)
+            for i, (dst, src) in enumerate(pairs):
+                items[i] = (dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size())
+            done = sb.submit(items, _current_stream_handle())
+            if self._trace_ref is not None:
+                self._trace_d2h.append((nbytes, done, None, kind))
+        else:
+            cs = self._copy_stream.cuda_stream
+            self._fence_copy_stream(cs)
+            t_start = None
+            if self._trace_ref is not None:
+                t_start = NativeEvent(timing=True)
+                t_start.record(cs)
+            for dst, src in pairs:
+                self._check_copy(_native.lib().sh_memcpy_d2h_async(dst.data_ptr(), src.data_ptr(),
+                                                                   src.numel() * src.element_size(), cs), kind, "d2h")
+            done = NativeEvent()
+            done.record(cs)
+            if t_start is not None:
+                t_end = NativeEvent(timing=True)
+                t_end.record(cs)
+                self._trace_d2h.append((nbytes, t_start, t_end, kind))
         self.bytes_d2h += nbytes
-        ev = NativeEvent()
-        ev.record(cs)
-        if t_start is not None:
-            t_end = NativeEvent(timing=True)
-            t_end.record(cs)
-            self._trace_d2h.append((nbytes, t_start, t_end, "block"))
         with self._lock:
-            self._pending_d2h.append((ev, [src, dst]))
-        return ev
+            self._pending_d2h.append((done, keep, 0))
+        return done
+
+    def release_with_copy(self, ev: "NativeEvent | SaveBackTicket", nbytes: int) -> bool:
+        """Counts ``nbytes`` of device memory as released from now on; the memory is freed when
+        the save-back copy that ``ev`` completes is reaped (the copy holds it until then).
+
+        The reference's save-back is synchronous, so its eviction loop sees the block's memory
+        gone before it checks the low watermark again (src/stagehand/scheduler.py:1216-1226 and
+        the loop at :1176-1182). Here the copy is still running, so the budget subtracts these
+        bytes (:meth:`releasing_bytes`): otherwise one eviction round would evict every
+        candidate. Returns False (nothing counted) when ``ev`` is not a save-back in flight.
+        """
+        if nbytes <= 0:
+            return False
+        with self._lock:
+            for i in range(len(self._pending_d2h) - 1, -1, -1):
+                e, keep, rel = self._pending_d2h[i]
+                if e is ev:
+                    self._pending_d2h[i] = (e, keep, rel + int(nbytes))
+                    self._releasing_bytes += int(nbytes)
+                    return True
+        return False
+
+    def releasing_bytes(self) -> int:
+        """Device bytes given up with save-back copies that have not been reaped yet."""
+        return self._releasing_bytes
 
     def _reap_d2h(self, block: bool = False) -> None:
         """Drops the device references of completed save-back copies (they complete in order)."""
@@ -523,14 +708,14 @@ class AsyncTransferEngine:
             with self._lock:
                 if not self._pending_d2h:
                     return
-                ev, _keep = self._pending_d2h[0]
+                ev = self._pending_d2h[0][0]
             if block:
                 ev.synchronize()
             elif not ev.query():
                 return
             with self._lock:
                 if self._pending_d2h and self._pending_d2h[0][0] is ev:
-                    self._pending_d2h.pop(0)
+                    self._releasing_bytes -= self._pending_d2h.pop(0)[2]
 
     # ── completion ───────────────────────────────────────────────────
 
@@ -619,6 +804,9 @@ class AsyncTransferEngine:
             if self._loader is not None:
                 _native.call("sh_loader_destroy", self._loader)
                 self._loader = None
+            if self._saveback is not None:
+                self._saveback.close()
+                self._saveback = None
             if self._owned_stream is not None:
                 _native.call("sh_stream_sync", self._owned_stream)
                 _native.call("sh_stream_destroy", self._owned_stream)

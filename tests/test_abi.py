@@ -53,6 +53,45 @@ def test_struct_sizes_match_header():
     assert PLAN_INFO_DTYPE.itemsize == 56
 
 
+def test_struct_mirrors_match_the_c_layout(tmp_path):
+    """Every numpy mirror of a header struct has the C compiler's size and field offsets
+    (compiled against include/stagehand_native.h with gcc)."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is not available")
+    mirrors = {
+        "sh_unpack_desc": _native.DESC_DTYPE,
+        "sh_plan_info": _native.PLAN_INFO_DTYPE,
+        "sh_load_request": _native.LOAD_REQUEST_DTYPE,
+        "sh_copy_item": _native.COPY_ITEM_DTYPE,
+        "sh_file_range": _native.FILE_RANGE_DTYPE,
+        "sh_file_info": _native.FILE_INFO_DTYPE,
+        "sh_pool_stats": _native.POOL_STATS_DTYPE,
+        "sh_vmm_stats": _native.VMM_STATS_DTYPE,
+        "sh_vmm_region_stats": _native.VMM_REGION_DTYPE,
+    }
+    lines = ['#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for struct, dt in mirrors.items():
+        lines.append(f'  printf("{struct} (sizeof) %zu\\n", sizeof({struct}));')
+        for name in dt.names:
+            lines.append(f'  printf("{struct} {name} %zu\\n", offsetof({struct}, {name}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-o", str(exe), str(src)], check=True, capture_output=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        struct, field, value = line.split()
+        got[(struct, field)] = int(value)
+    for struct, dt in mirrors.items():
+        assert got[(struct, "(sizeof)")] == dt.itemsize, struct
+        for name in dt.names:
+            assert got[(struct, name)] == dt.fields[name][1], (struct, name)
+
+
 def describe(rows) -> dict:
     table = make_descs(rows)
     info = np.zeros(1, dtype=PLAN_INFO_DTYPE)

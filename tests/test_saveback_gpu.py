@@ -1,0 +1,158 @@
+"""The SDMA save-back engine (native ``sh_saveback``) and the transfer engine's use of it.
+
+Save-back copies move evicted blocks' device bytes into pinned host memory (the
+reference's synchronous ``param.data.to("cpu")``, src/stagehand/scheduler.py:1216-1226).
+Here they run on a system DMA engine: ordered after the work queued on a stream
+before the submit, completing in submission order, and waited for by the loader
+when a load reads what they wrote. Every case checks bytes bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from stagehand_amd import _native
+from stagehand_amd._native import COPY_ITEM_DTYPE
+from stagehand_amd.pool import PinnedPool
+from stagehand_amd.transfer import AsyncTransferEngine, BlockSource, NativeEvent, SaveBackEngine, SaveBackTicket
+
+pytestmark = pytest.mark.gpu
+
+
+def _items(pairs: list[tuple[torch.Tensor, torch.Tensor]]) -> np.ndarray:
+    items = np.zeros(len(pairs), dtype=COPY_ITEM_DTYPE)
+    for i, (dst, src) in enumerate(pairs):
+        items[i] = (dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size())
+    return items
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_copies_land_bit_exact():
+    """Sizes from one byte to tens of MiB, odd lengths and offsets, several copies per ticket."""
+    g = torch.Generator(device="cuda").manual_seed(1)
+    sizes = [1, 15, 4096, 4097, (1 << 20) + 3, (48 << 20) + 5]
+    srcs = [torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g) for n in sizes]
+    dsts = [torch.zeros(n + 7, dtype=torch.uint8, pin_memory=True)[3:3 + n] for n in sizes]
+    sb = SaveBackEngine(torch.cuda.current_device())
+    one = sb.submit(_items([(dsts[0], srcs[0])]), _stream())
+    rest = sb.submit(_items(list(zip(dsts[1:], srcs[1:]))), _stream())
+    rest.synchronize()
+    assert one.query() and rest.query()
+    for d, s in zip(dsts, srcs):
+        assert torch.equal(d, s.cpu())
+    sb.close()
+
+
+def test_copies_read_what_the_stream_wrote_before_the_submit():
+    """The submit is issued while kernels that produce the source are still queued: the copy
+    waits for them (the worker waits for the event recorded at submit)."""
+    n = 32 << 20
+    a = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
+    src = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(n, dtype=torch.uint8, pin_memory=True)
+    sb = SaveBackEngine(torch.cuda.current_device())
+    for rep in range(3):
+        torch.cuda.synchronize()
+        y = a
+        for _ in range(12):  # keep the stream busy for a while
+            y = (y @ a) * 1e-3
+        src.copy_(y.view(torch.uint8).reshape(-1)[:n])
+        src.add_(rep + 1)
+        t = sb.submit(_items([(dst, src)]), _stream())
+        t.synchronize()
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src.cpu()), rep
+    sb.close()
+
+
+def test_tickets_complete_in_order_release_and_errors():
+    g = torch.Generator(device="cuda").manual_seed(2)
+    srcs = [torch.randint(0, 256, (8 << 20,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(3)]
+    dsts = [torch.zeros(8 << 20, dtype=torch.uint8, pin_memory=True) for _ in range(3)]
+    sb = SaveBackEngine(torch.cuda.current_device())
+    tickets = [sb.submit(_items([(d, s)]), _stream()) for d, s in zip(dsts, srcs)]
+    tickets[-1].synchronize()  # covers the earlier tickets
+    for d, s in zip(dsts, srcs):
+        assert torch.equal(d, s.cpu())
+    assert all(t.query() for t in tickets)
+    lib, h = _native.lib(), sb.handle
+    assert lib.sh_saveback_release(h, tickets[0].ticket) == _native.SH_OK
+    assert lib.sh_saveback_release(h, tickets[0].ticket) == _native.SH_OK  # twice: a no-op
+    assert lib.sh_saveback_query(h, 10**9) == _native.SH_ERR_INVALID
+    with pytest.raises(ValueError):
+        _native.call("sh_saveback_wait", h, 0)
+    bad = np.zeros(1, dtype=COPY_ITEM_DTYPE)
+    bad[0] = (0, srcs[0].data_ptr(), 16)
+    with pytest.raises(ValueError):
+        sb.submit(bad, _stream())
+    empty = sb.submit(np.zeros(0, dtype=COPY_ITEM_DTYPE), _stream())
+    empty.synchronize()
+    sb.close()
+    assert tickets[1].query()  # a closed engine waited for every copy
+    tickets[1].synchronize()
+
+
+def test_close_issues_and_waits_for_queued_copies():
+    g = torch.Generator(device="cuda").manual_seed(3)
+    src = torch.randint(0, 256, (96 << 20,), dtype=torch.uint8, device="cuda", generator=g)
+    dst = torch.zeros(96 << 20, dtype=torch.uint8, pin_memory=True)
+    sb = SaveBackEngine(torch.cuda.current_device())
+    sb.submit(_items([(dst, src)]), _stream())
+    sb.close()
+    assert torch.equal(dst, src.cpu())
+
+
+@pytest.mark.parametrize("mode", ["sdma", "stream"])
+def test_engine_save_backs_then_load_waits_for_them(mode):
+    """``d2h_async`` / ``d2h_into`` on either engine, then a load whose pinned pieces are the
+    save-back's outputs, submitted before the save-back finished: the load waits for it (in the
+    loader's worker for a ticket, on the device for an event)."""
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool, save_back=mode)
+    kind = SaveBackTicket if mode == "sdma" else NativeEvent
+    g = torch.Generator(device="cuda").manual_seed(4)
+    a = torch.randint(0, 256, (3 << 19,), dtype=torch.uint8, device="cuda", generator=g)
+    b = torch.randint(0, 256, (5000,), dtype=torch.uint8, device="cuda", generator=g)
+    (ha, hb), done = eng.d2h_async([a, b])
+    assert isinstance(done, kind)
+    block = torch.randint(0, 256, ((24 << 20) + 6,), dtype=torch.uint8, device="cuda", generator=g)
+    home = torch.zeros(block.numel() + 10, dtype=torch.uint8, pin_memory=True)
+    done2 = eng.d2h_into(block, home[:block.numel()])
+    assert isinstance(done2, kind)
+    pageable = torch.randint(0, 256, ((5 << 19) + 7,), dtype=torch.uint8)
+    layout = [(0, home[:block.numel()]), (block.numel(), ha), (block.numel() + ha.numel(), pageable),
+              (block.numel() + ha.numel() + pageable.numel(), hb)]
+    total = sum(t.numel() for _o, t in layout)
+    dst = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    h = eng.submit_block_load("mixed", BlockSource(layout, total), dst, wait_event=done2)
+    eng.wait(h)
+    assert torch.equal(dst.cpu(), torch.cat([block.cpu(), a.cpu(), pageable, b.cpu()]))
+    assert eng.bytes_d2h == a.numel() + b.numel() + block.numel()
+    eng.shutdown()
+    pool.shutdown()
+
+
+def test_trace_reports_copy_engine_spans():
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool, save_back="sdma")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    srcs = [torch.randint(0, 256, (64 << 20,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(3)]
+    homes = [torch.zeros(64 << 20, dtype=torch.uint8, pin_memory=True) for _ in range(3)]
+    eng.start_trace()
+    for s, h in zip(srcs, homes):
+        eng.d2h_into(s, h)
+    tr = eng.stop_trace()
+    spans = [(n, t0, t1) for n, t0, t1, kind in tr["d2h"] if kind == "block"]
+    assert len(spans) == 3
+    for n, t0, t1 in spans:
+        assert n == 64 << 20
+        assert -1.0 < t0 < t1 < 10_000.0
+        assert n / ((t1 - t0) * 1e-3) < 100e9  # no faster than a PCIe link can go
+    for s, h in zip(srcs, homes):
+        assert torch.equal(h, s.cpu())
+    eng.shutdown()
+    pool.shutdown()

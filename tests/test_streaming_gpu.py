@@ -293,13 +293,14 @@ def _train_dit(seed: int):
     return init_train_dit_(TrainDiT(depth=4, hidden=128, heads=4, mlp_ratio=2.0, rank=8), seed)
 
 
-@pytest.mark.parametrize("frozen_host_copies", [False, True])
-def test_checkpointed_lora_training_round_trip(frozen_host_copies):
+@pytest.mark.parametrize("frozen_host_copies,save_back", [(False, "sdma"), (True, "sdma"), (False, "stream")])
+def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back):
     """Config-5 shape in small: frozen base weights, trainable LoRA, activation checkpointing
     (blocks recomputed in backward under the runtime's hooks), module-backed eviction every
     block, an SGD step on the LoRA parameters between steps. Outputs, LoRA gradients and the
     updated LoRA weights match the same model trained unstreamed; with frozen host copies the
-    frozen weights are not copied back at eviction."""
+    frozen weights are not copied back at eviction. Save-backs on the SDMA engine and on the copy
+    stream."""
     from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN
 
     model = _train_dit(5)
@@ -311,7 +312,7 @@ def test_checkpointed_lora_training_round_trip(frozen_host_copies):
     target = torch.randn(1, 32, 128, generator=g).cuda()
     base_mb = torch.cuda.memory_allocated() / 2**20
     cfg = _config(vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb), prefetch_window_blocks=1,
-                  frozen_host_copies=frozen_host_copies)
+                  frozen_host_copies=frozen_host_copies, save_back_engine=save_back)
     rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
                                     inference_mode=False)
     lora = [p for n, p in model.named_parameters() if "lora" in n]
