@@ -993,7 +993,16 @@ def dit_leg(kind: str, args) -> dict:
         res["readers"] = readers_leg(args, src, reader)
     if kind == "file" and not args.skip_cpu:
         log("cpu baseline: the reference's config-3 block loads on a sample")
-        res["reference_staging_path"] = cpu_reference_config3_step(src)
+        ref3 = cpu_reference_config3_step(src)
+        staged = res.get("staged") or res.get("pinned")
+        if staged and staged.get("pcie_bytes_per_step"):
+            # the reference evicts synchronously down to the low watermark, so it would move the
+            # bytes the device path moves; its staging and H2D costs scale with them
+            frac = staged["pcie_bytes_per_step"] / ref3["pcie_bytes_per_step"]
+            ref3["device_traffic_fraction"] = round(frac, 4)
+            ref3["ms_per_step_overlapped_at_device_traffic"] = round(ref3["ms_per_step_overlapped"] * frac, 1)
+            ref3["ms_per_step_serial_at_device_traffic"] = round(ref3["ms_per_step_serial"] * frac, 1)
+        res["reference_staging_path"] = ref3
     if kind == "squareq" and args.squareq_v2 == "on":
         from stagehand_amd.squareq_v2 import write_v2_slab
 
