@@ -410,12 +410,14 @@ int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64_t* out2);
  * surface turbo_src/lib.rs:14-126). Every block's parameters live in ONE
  * pinned host region (params at 256-byte aligned offsets), so a block moves in
  * one hipMemcpyAsync when its slot is a contiguous device buffer
- * (sh_turbo_set_slot_buffer). Ordering is device-side only: the compute stream
- * waits on the block's own H2D event (no host synchronisation, no shared
- * event), an eviction orders its D2H after the compute queued so far, and a
- * slot freed by an eviction is reused by a prefetch through a device wait on
- * the slot's fence. Blocks marked write-back off (frozen weights) skip the
- * D2H. Device pointers in slots belong to the caller (PyTorch tensors),
+ * (sh_turbo_set_slot_buffer). The compute stream waits on the block's own H2D
+ * event (no host synchronisation, no shared event), an eviction orders its
+ * write-back after the compute queued so far, and a slot freed by an eviction
+ * is reused by a prefetch through a device wait on the slot's fence; a
+ * write-back on the SDMA engine (sh_turbo_set_save_back) is waited for on the
+ * host by the prefetch that reuses its slot or reloads its block. Blocks marked
+ * write-back off (frozen weights) skip the D2H and keep every wait on the
+ * device. Device pointers in slots belong to the caller (PyTorch tensors),
  * pinned host memory to the engine (engine.rs:132-138, 396-422).
  * Errors: a bad direction is SH_ERR_INVALID (ValueError, lib.rs:59-61); every
  * other failure, including "No free GPU slots" (engine.rs:189) and an index
@@ -443,6 +445,12 @@ int sh_turbo_param_offset(sh_turbo* t, uint32_t block, uint32_t param, uint64_t*
 /* No reference counterpart (the reference always copies back): 0 skips the
  * D2H at eviction for a block whose device copy is never written. */
 int sh_turbo_set_writeback(sh_turbo* t, uint32_t block, int enable);
+/* No reference counterpart: before sh_turbo_initialize, where write-backs run.
+ * 1 (the default): on an SDMA engine (sh_saveback); a prefetch that reuses the
+ * slot of a block being written back, or reloads that block, waits for the copy
+ * on the host. 0: hipMemcpyAsync on the engine's evict stream (a kernel on the
+ * compute units), ordered on the device only. */
+int sh_turbo_set_save_back(sh_turbo* t, int sdma);
 int sh_turbo_block_slot(sh_turbo* t, uint32_t block, int32_t* slot);     /* -1: none, engine.rs:375-378 */
 int sh_turbo_block_location(sh_turbo* t, uint32_t block, int* location); /* engine.rs:384-393 */
 int sh_turbo_counts(sh_turbo* t, uint32_t* blocks, uint32_t* slots, uint32_t* free_slots); /* engine.rs:380-382 */

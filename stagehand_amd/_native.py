@@ -170,6 +170,7 @@ _SIGNATURES: dict[str, list] = {
     "sh_turbo_destroy": [_vp],
     "sh_turbo_register_block": [_vp, _vp, _u32, ctypes.POINTER(_u32)],
     "sh_turbo_initialize": [_vp, _i32, _u32],
+    "sh_turbo_set_save_back": [_vp, _i32],
     "sh_turbo_stage_block": [_vp, _u32, _vp, _u32],
     "sh_turbo_step": [_vp, _u32, _i32, _vp],
     "sh_turbo_evict_sync": [_vp, _u32, _vp],

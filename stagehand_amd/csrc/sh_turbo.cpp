@@ -17,8 +17,16 @@
 //    makes the prefetch stream wait for that fence instead of the host
 //    draining the eviction stream first;
 //  * write-back can be switched off per block (frozen weights are not copied
-//    back to host memory on every eviction).
+//    back to host memory on every eviction);
+//  * write-back copies run on an SDMA engine (sh_saveback), not as
+//    hipMemcpyAsync on the evict stream: HIP runs a pinned device-to-host copy
+//    as a kernel on the compute units, and the compute kernels beside it run
+//    many times slower. A prefetch that reuses the slot of a block being
+//    written back, or reloads that block, then waits for the copy on the host
+//    (an SDMA copy has no device-side wait). Tickets complete in order, so
+//    the engine tracks the highest one known complete and releases the rest.
 #include <algorithm>
+#include <deque>
 #include <mutex>
 #include <vector>
 
@@ -40,6 +48,7 @@ struct Block {
   bool writeback = true;
   hipEvent_t h2d = nullptr;  // recorded after the block's H2D on the prefetch stream
   hipEvent_t d2h = nullptr;  // recorded after the block's eviction on the evict stream
+  uint64_t d2h_ticket = 0;   // its write-back on the save-back engine (0: none pending)
   hipEvent_t t_start = nullptr, t_end = nullptr;  // timing events around the last H2D (timing mode)
   bool timed = false;
 };
@@ -52,6 +61,7 @@ struct Slot {
   int assigned = -1;
   hipEvent_t fence = nullptr;   // the last eviction out of this slot
   bool fenced = false;
+  uint64_t fence_ticket = 0;    // that eviction's write-back on the save-back engine (0: none)
 };
 
 }  // namespace
@@ -64,6 +74,10 @@ struct sh_turbo {
   hipStream_t prefetch = nullptr;
   hipStream_t evict = nullptr;
   hipEvent_t compute_mark = nullptr;
+  sh_saveback* sb = nullptr;      // write-backs on an SDMA engine (null: on the evict stream)
+  bool sdma = true;               // sh_turbo_set_save_back
+  std::deque<uint64_t> tickets;   // write-back tickets not yet released, in order
+  uint64_t done_upto = 0;         // every ticket <= this one is complete (and released)
   int device = 0;
   bool initialized = false;
   bool timing = false;
@@ -141,6 +155,63 @@ int copy_block(sh_turbo* t, const Block& b, const Slot& s, bool to_device, hipSt
   return SH_OK;
 }
 
+// Releases the write-back tickets that have completed (they complete in order).
+int reap_tickets(sh_turbo* t) {
+  while (!t->tickets.empty()) {
+    const uint64_t tk = t->tickets.front();
+    int st = sh_saveback_query(t->sb, tk);
+    if (st == SH_ERR_NOT_READY) break;
+    if (st != SH_OK) return st;
+    t->done_upto = tk;
+    t->tickets.pop_front();
+    st = sh_saveback_release(t->sb, tk);
+    if (st != SH_OK) return st;
+  }
+  return SH_OK;
+}
+
+bool ticket_done(sh_turbo* t, uint64_t tk) {
+  if (tk == 0 || tk <= t->done_upto) return true;
+  if (reap_tickets(t) != SH_OK) return false;  // the failure surfaces in the next wait
+  return tk <= t->done_upto;
+}
+
+// Host wait for a write-back ticket (and every earlier one), then releases them.
+int wait_ticket(sh_turbo* t, uint64_t tk) {
+  if (tk == 0 || tk <= t->done_upto) return SH_OK;
+  int st = sh_saveback_wait(t->sb, tk);
+  if (st != SH_OK) return st;
+  return reap_tickets(t);
+}
+
+// The write-back copies of block b out of slot s: one item for a contiguous
+// slot, else one per run of parameters contiguous on both sides.
+std::vector<sh_copy_item> writeback_items(sh_turbo* t, const Block& b, const Slot& s) {
+  std::vector<sh_copy_item> items;
+  if (s.base) {
+    if (b.extent) items.push_back({b.host, s.base, b.extent});
+    t->bytes_d2h += b.extent;
+    return items;
+  }
+  size_t p = 0, n = b.sizes.size();
+  while (p < n) {
+    if (b.sizes[p] == 0) { ++p; continue; }
+    uint8_t* dev = static_cast<uint8_t*>(s.ptrs[p]);
+    uint8_t* host = b.host + b.offsets[p];
+    uint64_t len = b.sizes[p];
+    size_t q = p + 1;
+    while (q < n && b.sizes[q] != 0 && static_cast<uint8_t*>(s.ptrs[q]) == dev + len &&
+           b.host + b.offsets[q] == host + len) {
+      len += b.sizes[q];
+      ++q;
+    }
+    items.push_back({host, dev, len});
+    t->bytes_d2h += len;
+    p = q;
+  }
+  return items;
+}
+
 // A free slot for block b: one whose fence has passed if any, else the one
 // released first (the prefetch stream then waits for its fence on the device).
 int take_slot(sh_turbo* t, uint32_t b, int* out) {
@@ -151,7 +222,7 @@ int take_slot(sh_turbo* t, uint32_t b, int* out) {
   size_t pick = 0;
   for (size_t i = 0; i < t->free_slots.size(); ++i) {
     Slot& s = t->slots[t->free_slots[i]];
-    if (!s.fenced || hipEventQuery(s.fence) == hipSuccess) { pick = i; break; }
+    if ((!s.fenced || hipEventQuery(s.fence) == hipSuccess) && ticket_done(t, s.fence_ticket)) { pick = i; break; }
   }
   int si = t->free_slots[pick];
   int rc = check_slot_fits(t->slots[si], blk, (uint32_t)si);
@@ -171,11 +242,20 @@ int async_prefetch(sh_turbo* t, uint32_t b) {
   if (rc != SH_OK) return rc;
   Slot& s = t->slots[si];
   // the pinned region may still be the target of this block's write-back
-  if (blk.location == SH_TURBO_D2H) SH_HIP(hipStreamWaitEvent(t->prefetch, blk.d2h, 0));
+  if (blk.location == SH_TURBO_D2H) {
+    SH_HIP(hipStreamWaitEvent(t->prefetch, blk.d2h, 0));
+    rc = wait_ticket(t, blk.d2h_ticket);
+    if (rc != SH_OK) return rc;
+    blk.d2h_ticket = 0;
+  }
   if (s.fenced) {
     SH_HIP(hipStreamWaitEvent(t->prefetch, s.fence, 0));
     s.fenced = false;
   }
+  // the slot may still be the source of the previous block's write-back
+  rc = wait_ticket(t, s.fence_ticket);
+  if (rc != SH_OK) return rc;
+  s.fence_ticket = 0;
   if (t->timing) SH_HIP(hipEventRecord(blk.t_start, t->prefetch));
   rc = copy_block(t, blk, s, true, t->prefetch);
   if (rc != SH_OK) return rc;
@@ -198,13 +278,21 @@ int async_evict(sh_turbo* t, uint32_t b, hipStream_t compute) {
   SH_HIP(hipEventRecord(t->compute_mark, compute));
   SH_HIP(hipStreamWaitEvent(t->evict, t->compute_mark, 0));
   SH_HIP(hipStreamWaitEvent(t->evict, blk.h2d, 0));
-  if (blk.writeback) {
+  uint64_t ticket = 0;
+  if (blk.writeback && t->sb) {
+    std::vector<sh_copy_item> items = writeback_items(t, blk, s);
+    int rc = sh_saveback_submit(t->sb, items.data(), items.size(), t->evict, &ticket);
+    if (rc != SH_OK) return rc;
+    t->tickets.push_back(ticket);
+  } else if (blk.writeback) {
     int rc = copy_block(t, blk, s, false, t->evict);
     if (rc != SH_OK) return rc;
   }
   SH_HIP(hipEventRecord(blk.d2h, t->evict));
   SH_HIP(hipEventRecord(s.fence, t->evict));
   s.fenced = true;
+  s.fence_ticket = ticket;
+  blk.d2h_ticket = ticket;
   s.assigned = -1;
   t->free_slots.push_back(blk.slot);
   blk.slot = -1;
@@ -226,15 +314,27 @@ int sync_prefetch(sh_turbo* t, uint32_t b, hipStream_t compute) {
 
 int sync_evict(sh_turbo* t) {
   SH_HIP(hipStreamSynchronize(t->evict));
-  for (Block& blk : t->blocks)
+  if (!t->tickets.empty()) {
+    int rc = wait_ticket(t, t->tickets.back());
+    if (rc != SH_OK) return rc;
+  }
+  for (Block& blk : t->blocks) {
     if (blk.location == SH_TURBO_D2H) blk.location = SH_TURBO_CPU;
-  for (Slot& s : t->slots) s.fenced = false;
+    blk.d2h_ticket = 0;
+  }
+  for (Slot& s : t->slots) {
+    s.fenced = false;
+    s.fence_ticket = 0;
+  }
   return SH_OK;
 }
 
 // d2h → cpu once the eviction has finished (the reference flips it in sync_evict)
 void settle(sh_turbo* t, Block& blk) {
-  if (blk.location == SH_TURBO_D2H && hipEventQuery(blk.d2h) == hipSuccess) blk.location = SH_TURBO_CPU;
+  if (blk.location == SH_TURBO_D2H && hipEventQuery(blk.d2h) == hipSuccess && ticket_done(t, blk.d2h_ticket)) {
+    blk.location = SH_TURBO_CPU;
+    blk.d2h_ticket = 0;
+  }
 }
 
 }  // namespace
@@ -254,6 +354,7 @@ extern "C" int sh_turbo_destroy(sh_turbo* t) {
     (void)hipStreamSynchronize(t->prefetch);
     (void)hipStreamSynchronize(t->evict);
   }
+  if (t->sb) (void)sh_saveback_destroy(t->sb);  // waits for every write-back first
   for (Block& b : t->blocks) {
     if (b.host) (void)hipHostFree(b.host);
     if (b.h2d) (void)hipEventDestroy(b.h2d);
@@ -297,6 +398,10 @@ extern "C" int sh_turbo_initialize(sh_turbo* t, int device, uint32_t window) {
   SH_HIP(hipStreamCreateWithFlags(&t->prefetch, hipStreamNonBlocking));
   SH_HIP(hipStreamCreateWithFlags(&t->evict, hipStreamNonBlocking));
   SH_HIP(hipEventCreateWithFlags(&t->compute_mark, hipEventDisableTiming));
+  if (t->sdma) {
+    int rc = sh_saveback_create(device, &t->sb);
+    if (rc != SH_OK) return rc;
+  }
   size_t max_params = 0;
   for (const Block& b : t->blocks) max_params = std::max(max_params, b.sizes.size());
   std::vector<uint64_t> cap(max_params, 0);
@@ -320,6 +425,15 @@ extern "C" int sh_turbo_initialize(sh_turbo* t, int device, uint32_t window) {
     t->slots.push_back(std::move(s));
   }
   t->initialized = true;
+  return SH_OK;
+}
+
+extern "C" int sh_turbo_set_save_back(sh_turbo* t, int sdma) {
+  sh::clear_error();
+  if (!t) return sh::fail(SH_ERR_INVALID, "sh_turbo_set_save_back: null engine");
+  std::lock_guard<std::mutex> g(t->mu);
+  if (t->initialized) return sh::fail(SH_ERR_STATE, "set_save_back after initialize");
+  t->sdma = sdma != 0;
   return SH_OK;
 }
 

@@ -8,7 +8,8 @@ compute stream; the torch current stream by default) because the engine
 orders compute after a block's copy on the device instead of blocking the
 host. Extra methods: ``set_slot_buffer`` / ``slot_bytes`` /
 ``param_offset`` (a slot as one contiguous buffer, a block in one copy),
-``set_writeback`` (no D2H for frozen blocks) and ``bytes_moved``.
+``set_writeback`` (no D2H for frozen blocks), ``set_save_back`` (write-backs on
+an SDMA engine or the evict stream) and ``bytes_moved``.
 
 ``TurboConductor`` keeps the reference's conductor interface
 (src/stagehand/turbo.py:29-201): discover blocks by pattern, ``prepare`` them
@@ -72,6 +73,13 @@ class TransferEngine:
         idx = ctypes.c_uint32()
         _native.call("sh_turbo_register_block", self._handle(), sizes.ctypes.data, sizes.size, ctypes.byref(idx))
         return idx.value
+
+    def set_save_back(self, engine: str) -> None:
+        """Before ``initialize``: write-backs on an SDMA engine ("sdma", the default) or as
+        ``hipMemcpyAsync`` on the engine's evict stream ("stream")."""
+        if engine not in ("sdma", "stream"):
+            raise ValueError(f"save_back must be 'sdma' or 'stream', got {engine!r}")
+        _native.call("sh_turbo_set_save_back", self._handle(), int(engine == "sdma"))
 
     def initialize(self, device: int, window_size: int) -> None:
         _native.call("sh_turbo_initialize", self._handle(), int(device), int(window_size))
@@ -178,14 +186,18 @@ class TurboConductor:
 
     def __init__(self, model: nn.Module, block_pattern: str = r".*\.block\.\d+$", dtype: torch.dtype = torch.bfloat16,
                  device: int = 0, vram_budget_gb: float = 18.0, *, contiguous_slots: bool = True,
-                 writeback: str = "auto") -> None:
+                 writeback: str = "auto", save_back: str = "sdma") -> None:
         """``contiguous_slots=False`` gives every parameter position its own slot tensor, as
         src/stagehand/turbo.py:123-147 does (one copy per parameter); ``writeback`` is
         "auto" (copy back only blocks with trainable parameters) or "always" (as
-        turbo_src/engine.rs:233-264 does)."""
+        turbo_src/engine.rs:233-264 does); ``save_back`` is where write-backs run
+        (``TransferEngine.set_save_back``)."""
         _native.lib()  # fail loudly without the native library
         if writeback not in ("auto", "always"):
             raise ValueError(f"writeback must be 'auto' or 'always', got {writeback!r}")
+        if save_back not in ("sdma", "stream"):
+            raise ValueError(f"save_back must be 'sdma' or 'stream', got {save_back!r}")
+        self._save_back = save_back
         self._contiguous = contiguous_slots
         self._writeback = writeback
         self._dtype = dtype
@@ -228,6 +240,7 @@ class TurboConductor:
             meta = [(n, tuple(p.shape), p.numel() * self._dtype.itemsize) for n, p in mod.named_parameters()]
             engine.register_block([m[2] for m in meta])
             self._param_meta.append(meta)
+        engine.set_save_back(self._save_back)
         engine.initialize(self._device_idx, self.WINDOW)
         for bi, mod in enumerate(self._block_modules):
             params = list(mod.named_parameters())

@@ -59,13 +59,15 @@ def _blocks(seed: int, n: int, sizes_fn):
 
 
 @pytest.mark.gpu
-def test_per_param_slots_land_every_byte():
+@pytest.mark.parametrize("save_back", ["sdma", "stream"])
+def test_per_param_slots_land_every_byte(save_back):
     """Reference usage: slot pointers per parameter position, sized to the largest block."""
     sizes = lambda i: [4096 + 512 * (i % 3), 1000 + i, 0, 77 * (i + 1)]  # ragged, one empty param
     data = _blocks(1, 7, sizes)
     e = TransferEngine()
     for d in data:
         e.register_block([t.numel() for t in d])
+    e.set_save_back(save_back)
     e.initialize(torch.cuda.current_device(), 3)
     assert (e.num_gpu_slots(), e.num_free_slots()) == (3, 3)
     for i, d in enumerate(data):
@@ -93,12 +95,14 @@ def test_per_param_slots_land_every_byte():
 
 
 @pytest.mark.gpu
-def test_contiguous_slots_one_copy_per_block_and_writeback():
+@pytest.mark.parametrize("save_back", ["sdma", "stream"])
+def test_contiguous_slots_one_copy_per_block_and_writeback(save_back):
     sizes = lambda i: [3000 + i, 5000, 123]
     data = _blocks(2, 5, sizes)
     e = TransferEngine()
     for d in data:
         e.register_block([t.numel() for t in d])
+    e.set_save_back(save_back)
     e.initialize(torch.cuda.current_device(), 3)
     for i, d in enumerate(data):
         e.stage_block(i, [t.data_ptr() for t in d])
@@ -131,6 +135,51 @@ def test_contiguous_slots_one_copy_per_block_and_writeback():
         if want_bump:
             want[0] += 1
         assert torch.equal(got, want), i
+    e.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("save_back", ["sdma", "stream"])
+def test_written_back_blocks_reload_with_their_updates(save_back):
+    """Forward: every block is changed on the device right after its step, with kernels still
+    queued when the next step evicts it. Backward: each block reloads from its written-back host
+    region (through slots that the write-backs were still reading) and carries the change."""
+    sizes = lambda i: [(1 << 20) + 4096 * i, 3 << 18, 999]
+    data = _blocks(3, 6, sizes)
+    e = TransferEngine()
+    for d in data:
+        e.register_block([t.numel() for t in d])
+    e.set_save_back(save_back)
+    e.initialize(torch.cuda.current_device(), 3)
+    for i, d in enumerate(data):
+        e.stage_block(i, [t.data_ptr() for t in d])
+    nb = e.slot_bytes()
+    slots = [torch.empty(nb, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    for s, t in enumerate(slots):
+        e.set_slot_buffer(s, t.data_ptr(), nb)
+    a = torch.randn(2048, 2048, device="cuda")
+    for rnd in range(2):
+        for direction, order in (("forward", range(6)), ("backward", reversed(range(6)))):
+            for i in order:
+                e.step(i, direction)
+                base = slots[e.block_slot(i)]
+                for _ in range(3):  # keep the compute stream busy past the next eviction
+                    a = (a @ a) * 1e-3
+                for p in range(3):
+                    off = e.param_offset(i, p)
+                    view = base[off:off + data[i][p].numel()]
+                    view.add_(1)
+                    data[i][p] += 1
+        torch.cuda.synchronize()
+    e.drain()
+    for i in range(6):
+        e.step(i, "forward")
+        torch.cuda.current_stream().synchronize()
+        base = slots[e.block_slot(i)]
+        for p, want in enumerate(data[i]):
+            off = e.param_offset(i, p)
+            assert torch.equal(base[off:off + want.numel()].cpu(), want), (i, p)
+    e.drain()
     e.close()
 
 
