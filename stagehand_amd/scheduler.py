@@ -922,6 +922,21 @@ class StagehandScheduler:
                 break
             self._evict_block(bid, save_back=not self._inference_mode)
             self._telemetry.record_eviction()
+            self._bound_save_back_backlog()
+
+    def _bound_save_back_backlog(self) -> None:
+        """Host wait for the oldest save-backs while the device memory they still hold exceeds
+        the gap between the watermarks. The budget counts that memory as released (the
+        reference's synchronous copy has freed it), so without a bound the memory actually
+        allocated could exceed the high watermark by the whole save-back backlog."""
+        wait = getattr(self._engine, "wait_releasing", None)
+        if wait is None:
+            return
+        high = getattr(self._budget, "high_watermark_mb", None)
+        low = getattr(self._budget, "low_watermark_mb", None)
+        if high is None or low is None:
+            return
+        wait(int((high - low) * 1024 * 1024))
 
     def _release_device_buffer(self, res_entry: ResidencyEntry) -> None:
         """Drop the block's device buffer; an unfinished load is waited for on the device first."""

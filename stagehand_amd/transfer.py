@@ -702,6 +702,18 @@ class AsyncTransferEngine:
         """Device bytes given up with save-back copies that have not been reaped yet."""
         return self._releasing_bytes
 
+    def wait_releasing(self, max_bytes: int) -> None:
+        """Waits on the host for the oldest save-backs until at most ``max_bytes`` of released
+        device memory is still held by copies in flight."""
+        self._reap_d2h()
+        while self._releasing_bytes > max_bytes:
+            with self._lock:
+                if not self._pending_d2h:
+                    return
+                ev = self._pending_d2h[0][0]
+            ev.synchronize()
+            self._reap_d2h()
+
     def _reap_d2h(self, block: bool = False) -> None:
         """Drops the device references of completed save-back copies (they complete in order)."""
         while True:
