@@ -194,6 +194,25 @@ class TestBudget:
             assert bm.can_prefetch() is prefetch
             assert bm.headroom_mb() == pytest.approx(100 - used_mb)
 
+    def test_memory_held_by_save_backs_counts_as_released(self):
+        """Device memory an eviction gave up, still held by its asynchronous save-back, is left out
+        (the reference's synchronous copy has freed it when the eviction loop checks again)."""
+        bm = BudgetManager(high_watermark_mb=100, low_watermark_mb=50)
+        releasing = [0]
+        bm.count_as_released(lambda: releasing[0])
+        with mock.patch("torch.cuda.is_available", return_value=True), \
+                mock.patch("torch.cuda.memory_allocated", return_value=120 << 20):
+            assert bm.above_high_watermark() and not bm.below_low_watermark()
+            releasing[0] = 80 << 20
+            assert bm.vram_used_mb() == pytest.approx(40.0)
+            assert bm.below_low_watermark() and not bm.above_high_watermark()
+            releasing[0] = 500 << 20  # never below zero
+            assert bm.vram_used_mb() == 0.0
+        bm.count_as_released(None)
+        with mock.patch("torch.cuda.is_available", return_value=True), \
+                mock.patch("torch.cuda.memory_allocated", return_value=120 << 20):
+            assert bm.vram_used_mb() == pytest.approx(120.0)
+
     def test_without_gpu(self):
         bm = BudgetManager(high_watermark_mb=100, low_watermark_mb=50)
         with mock.patch("torch.cuda.is_available", return_value=False):

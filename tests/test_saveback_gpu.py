@@ -156,3 +156,29 @@ def test_trace_reports_copy_engine_spans():
         assert torch.equal(h, s.cpu())
     eng.shutdown()
     pool.shutdown()
+
+
+@pytest.mark.parametrize("mode", ["sdma", "stream"])
+def test_released_memory_is_counted_until_reaped_and_bounded(mode):
+    """``release_with_copy`` counts a buffer as released while its save-back holds it;
+    ``wait_releasing`` waits for the oldest save-backs until at most the given bytes remain."""
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool, save_back=mode)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    n = 32 << 20
+    srcs = [torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(4)]
+    homes = [torch.zeros(n, dtype=torch.uint8, pin_memory=True) for _ in range(4)]
+    done = [eng.d2h_into(s, h) for s, h in zip(srcs, homes)]
+    assert all(eng.release_with_copy(d, n) for d in done)
+    assert not eng.release_with_copy(NativeEvent(), n)  # not a save-back in flight
+    assert eng.releasing_bytes() <= 4 * n
+    eng.wait_releasing(n)
+    assert eng.releasing_bytes() <= n
+    for d in done[:3]:
+        assert d.query()
+    eng.wait_releasing(0)
+    assert eng.releasing_bytes() == 0
+    for s, h in zip(srcs, homes):
+        assert torch.equal(h, s.cpu())
+    eng.shutdown()
+    pool.shutdown()
