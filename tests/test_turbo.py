@@ -47,6 +47,13 @@ def test_conductor_needs_matching_blocks():
         TurboConductor(torch.nn.Linear(4, 4), block_pattern=r"^nothing$")
 
 
+def test_conductor_rejects_a_window_below_three():
+    with pytest.raises(ValueError, match="window must be at least 3"):
+        TurboConductor(torch.nn.Sequential(torch.nn.Linear(4, 4)), block_pattern=r"^0$", window=2)
+    with pytest.raises(ValueError, match="save_back"):
+        TurboConductor(torch.nn.Sequential(torch.nn.Linear(4, 4)), block_pattern=r"^0$", save_back="dma")
+
+
 # ── GPU ─────────────────────────────────────────────────────────────────
 
 
@@ -229,6 +236,35 @@ def test_conductor_forward_matches_resident_model():
     # copy of the block's aligned extent each
     assert h2d == (6 + 5 + 5) * cond.engine.slot_bytes()
     assert cond.engine.slot_bytes() >= sum(p.numel() * 2 for p in ref.blocks[0].parameters())
+    for h in handles:
+        h.remove()
+    cond.shutdown()
+    for p, q in zip(model.parameters(), ref.parameters()):
+        assert torch.equal(p.view(torch.int16), q.cpu().view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("window", [3, 4])
+def test_conductor_with_writeback_and_other_windows_matches_resident_model(window):
+    """Write-back of every block (the reference's engine) through 3 or 4 slots: outputs match the
+    resident model and the host copies are unchanged after three passes."""
+    model = init_(TinyStack(n=6, hidden=64, mlp=4), seed=7).to(torch.bfloat16)
+    model.requires_grad_(False)
+    ref = init_(TinyStack(n=6, hidden=64, mlp=4), seed=7).to(device="cuda", dtype=torch.bfloat16)
+    x = torch.randn(8, 64, generator=torch.Generator().manual_seed(8)).to("cuda", torch.bfloat16)
+    cond = TurboConductor(model, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, writeback="always",
+                          window=window)
+    cond.prepare()
+    assert cond.engine.num_gpu_slots() == window
+    handles = cond.install_hooks()
+    with torch.no_grad():
+        outs = [model(x) for _ in range(3)]
+        want = ref(x)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), want.view(torch.int16))
+    h2d, d2h = cond.engine.bytes_moved()
+    assert d2h > 0
     for h in handles:
         h.remove()
     cond.shutdown()
