@@ -268,14 +268,17 @@ int async_prefetch(sh_turbo* t, uint32_t b) {
   return SH_OK;
 }
 
-int async_evict(sh_turbo* t, uint32_t b, hipStream_t compute) {
+// Evicts block b after the compute marked in t->compute_mark (recorded by the
+// caller once every kernel that may read the slot is queued, and before
+// anything later, such as the wait for the next block's H2D, is queued behind
+// it: an eviction ordered after that wait would serialise each write-back
+// behind the following load).
+int async_evict(sh_turbo* t, uint32_t b) {
   Block& blk = t->blocks[b];
   if (blk.location == SH_TURBO_CPU || blk.location == SH_TURBO_D2H) return SH_OK;
   if (blk.slot < 0) return SH_OK;
   Slot& s = t->slots[blk.slot];
-  // after every kernel queued so far on the compute stream (which may read the
-  // slot) and after the block's own H2D
-  SH_HIP(hipEventRecord(t->compute_mark, compute));
+  // after the marked compute and after the block's own H2D
   SH_HIP(hipStreamWaitEvent(t->evict, t->compute_mark, 0));
   SH_HIP(hipStreamWaitEvent(t->evict, blk.h2d, 0));
   uint64_t ticket = 0;
@@ -469,6 +472,9 @@ extern "C" int sh_turbo_step(sh_turbo* t, uint32_t block, int direction, void* c
   if (rc != SH_OK) return rc;
   SH_HIP(hipSetDevice(t->device));
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  // the previous block's last kernels are queued now; mark them before the
+  // compute stream is made to wait for this block's H2D
+  SH_HIP(hipEventRecord(t->compute_mark, compute));
   rc = sync_prefetch(t, block, compute);
   if (rc != SH_OK) return rc;
   const uint32_t n = (uint32_t)t->blocks.size();
@@ -476,7 +482,7 @@ extern "C" int sh_turbo_step(sh_turbo* t, uint32_t block, int direction, void* c
   const int64_t prev = fwd ? (int64_t)block - 1 : (int64_t)block + 1;
   const int64_t next = fwd ? (int64_t)block + 1 : (int64_t)block - 1;
   if (prev >= 0 && prev < n) {
-    rc = async_evict(t, (uint32_t)prev, compute);
+    rc = async_evict(t, (uint32_t)prev);
     if (rc != SH_OK) return rc;
   }
   if (next >= 0 && next < n) {
@@ -494,7 +500,8 @@ extern "C" int sh_turbo_evict_sync(sh_turbo* t, uint32_t block, void* compute_st
   if (rc == SH_OK) rc = check_block(t, block);
   if (rc != SH_OK) return rc;
   SH_HIP(hipSetDevice(t->device));
-  rc = async_evict(t, block, static_cast<hipStream_t>(compute_stream));
+  SH_HIP(hipEventRecord(t->compute_mark, static_cast<hipStream_t>(compute_stream)));
+  rc = async_evict(t, block);
   if (rc != SH_OK) return rc;
   return sync_evict(t);
 }

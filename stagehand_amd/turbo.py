@@ -192,9 +192,8 @@ class TurboConductor:
         "auto" (copy back only blocks with trainable parameters) or "always" (as
         turbo_src/engine.rs:233-264 does); ``save_back`` is where write-backs run
         (``TransferEngine.set_save_back``); ``window`` is the number of device slots (default
-        ``WINDOW``, the reference's 3). With write-back, every prefetch into a slot waits for
-        the write-back out of it, and a fourth slot lets the two directions overlap: the
-        config-3 model in the reference layout ran 833 ms per step with 3 slots, 499 ms with 4."""
+        ``WINDOW``, the reference's 3, at least 3). With write-back, every prefetch into a slot
+        waits for the write-back out of it; more slots give it more time."""
         _native.lib()  # fail loudly without the native library
         if writeback not in ("auto", "always"):
             raise ValueError(f"writeback must be 'auto' or 'always', got {writeback!r}")
