@@ -668,7 +668,10 @@ def train_leg(args) -> dict:
                        "bf16 block weights, LoRA r32 on self-attention q/k/v/o = 50.3 M trainable), batch 1 x 4096 "
                        "tokens + 512 conditioning tokens, MSE loss, SGD on LoRA, activation checkpointing, "
                        "VRAM budget 24 GB (watermarks 19200 / 14400 MB), prefetch window 3"}
-    for label, fhc in (("reference_eviction", False), ("frozen_host_copies", True)):
+    modes = (("reference_eviction", False), ("frozen_host_copies", True))
+    if args.train_modes == "reference":
+        modes = modes[:1]
+    for label, fhc in modes:
         t0 = time.perf_counter()
         with torch.device("meta"):
             model = TrainDiT()
@@ -677,7 +680,7 @@ def train_leg(args) -> dict:
         cfg = stagehand.StagehandConfig(pinned_pool_mb=4096, pinned_slab_mb=256, vram_high_watermark_mb=19200,
                                         vram_low_watermark_mb=14400, prefetch_window_blocks=3, max_inflight_transfers=4,
                                         nan_inf_check=False, strict_bf16=False, telemetry_enabled=True,
-                                        frozen_host_copies=fhc)
+                                        frozen_host_copies=fhc, save_back_engine=args.save_back)
         cfg.telemetry_file = None
         rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
                                         inference_mode=False)
@@ -1085,6 +1088,10 @@ def main() -> int:
     ap.add_argument("--only-dit", action="store_true", help="skip the config-2 kernel legs (profiling the DiT stream)")
     ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
     ap.add_argument("--train", default="on", choices=["on", "off"], help="config-5 streamed training step")
+    ap.add_argument("--train-modes", default="both", choices=["both", "reference"],
+                    help="config 5 with the reference's eviction and with frozen host copies, or the first only")
+    ap.add_argument("--save-back", default="sdma", choices=["sdma", "stream"],
+                    help="where config 5's save-back copies run (StagehandConfig.save_back_engine)")
     ap.add_argument("--vmm", default="on", choices=["on", "off"], help="config-3 DiT served from the VMM backend")
     ap.add_argument("--file-reader", default="pread", choices=["mmap", "pread", "direct"],
                     help="weight-file reader of the config-3 leg")
