@@ -202,7 +202,13 @@ class StagehandRuntime:
         handle = self._vmm.models[self._vmm_model_id]
         stream = torch.cuda.current_stream().cuda_stream
         tensor, ok = handle.get_block_tensor(idx, stream)
-        handle.prefetch_block(idx + 1, stream)  # the next block's fill runs while this one computes
+        # the next block's fill runs while this one computes; further blocks of the prefetch
+        # window only while they fit under the ceiling without evicting anything
+        handle.prefetch_block(idx + 1, stream)
+        for k in range(2, self._config.prefetch_window_blocks + 1):
+            if not handle.fits_without_eviction(idx + k):
+                break
+            handle.prefetch_block(idx + k, stream)
         if not ok:
             return False
         try:

@@ -392,6 +392,15 @@ class VmmModelHandle:
             for off, t in pieces:
                 dst[off:off + t.numel()].copy_(t, non_blocking=True)
 
+    def fits_without_eviction(self, block_idx: int) -> bool:
+        """True when the block's region fits beside everything mapped now, under the ceiling."""
+        if not 0 <= block_idx < self.block_count:
+            return False
+        st = self.allocator.stats()
+        g = max(1, int(st["granularity"]))
+        need = -(-int(self.block_sizes[block_idx]) // g) * g
+        return int(st["mapped_bytes"]) + need <= int(st["vram_ceiling"])
+
     def prefetch_block(self, block_idx: int, stream: int | None = None) -> None:
         """Maps the block's region ahead and warms its file pages (vmm_backend.py:283-291). With the
         block loader and a ``stream``, a region whose contents are stale is mapped now and its fill
