@@ -290,6 +290,9 @@ class StagehandScheduler:
                     targets.append(("grad", name))
         if not srcs:
             return
+        # a parameter viewing the block buffer is copied out of it on the device first, so the
+        # buffer is not held until the save-back completes (it is freed when the block is dropped)
+        srcs = [t if t.untyped_storage().nbytes() <= t.numel() * t.element_size() else t.clone() for t in srcs]
         outs, ev = self._engine.d2h_async(srcs)
         params = dict(module.named_parameters())
         for (what, name), out in zip(targets, outs):
@@ -333,8 +336,9 @@ class StagehandScheduler:
         return True
 
     def _release_with_save_back(self, block_id: str, res_entry: ResidencyEntry, fence_before: Any) -> None:
-        """The block's device buffer, about to be dropped, stays held by the save-back copy just
-        queued for it (its fence changed): count it as released for the budget from now on."""
+        """The block's device buffer, about to be dropped, stays held by the whole-block save-back
+        just queued for it (its fence changed): count it as released for the budget from now on.
+        Per-parameter save-backs copy views of the buffer out first and do not hold it."""
         fence = self._d2h_fences.get(block_id)
         gpu = res_entry.gpu_tensor
         if fence is None or fence is fence_before or gpu is None or not hasattr(self._engine, "release_with_copy"):
@@ -970,12 +974,15 @@ class StagehandScheduler:
                 self._residency.transition(block_id, BlockState.EVICTING)
                 self._await_pending_load(block_id)
                 fence_before = self._d2h_fences.get(block_id)
+                home = False
                 if module is not None:
                     names = self._take_host_copies(block_id, module, [n for n, _ in module.named_parameters()])
-                    if self._save_block_home(block_id, module, res_entry, names):
+                    home = self._save_block_home(block_id, module, res_entry, names)
+                    if home:
                         names = []
                     self._save_params_to_host(block_id, module, names, with_grads=True)
-                self._release_with_save_back(block_id, res_entry, fence_before)
+                if home:  # the whole-block copy reads the buffer until it completes
+                    self._release_with_save_back(block_id, res_entry, fence_before)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -986,7 +993,6 @@ class StagehandScheduler:
                 mutable = set(block_entry.module_param_names)
                 keep_on_gpu = self._defer_backward_eviction and not self._backward_phase
                 specs = {s.param_name: s for s in block_entry.file_param_specs}
-                fence_before = self._d2h_fences.get(block_id)
                 if module is not None and res_entry.param_layout is not None:
                     to_host = []
                     for name, _shape, dtype, _off, _numel in res_entry.param_layout:
@@ -1007,7 +1013,6 @@ class StagehandScheduler:
                     for name, param in module.named_parameters():
                         if name in mutable and param.grad is not None and param.grad.device.type != "cpu":
                             param.grad = param.grad.to("cpu", non_blocking=True)
-                self._release_with_save_back(block_id, res_entry, fence_before)
                 self._release_device_buffer(res_entry)
                 res_entry.param_layout = None
                 self._residency.transition(block_id, BlockState.UNLOADED)
@@ -1037,7 +1042,6 @@ class StagehandScheduler:
 
         # No save-back: GPU_READY → GPU_FREEING → UNLOADED.
         self._residency.transition(block_id, BlockState.GPU_FREEING)
-        fence_before = self._d2h_fences.get(block_id)
         if module is not None and res_entry.param_layout is not None:
             if module_backed:
                 self._await_pending_load(block_id)
@@ -1058,7 +1062,6 @@ class StagehandScheduler:
                 self._save_params_to_host(block_id, module, to_host)
             else:
                 _detach_params(module, res_entry.param_layout)
-        self._release_with_save_back(block_id, res_entry, fence_before)
         self._release_device_buffer(res_entry)
         res_entry.param_layout = None
         self._residency.transition(block_id, BlockState.UNLOADED)
