@@ -924,7 +924,7 @@ class StagehandScheduler:
         for _score, bid in scored:
             if self._budget.below_low_watermark():
                 break
-            self._evict_block(bid, save_back=not self._inference_mode)
+            self._evict_block_async(bid, save_back=not self._inference_mode)
             self._telemetry.record_eviction()
             self._bound_save_back_backlog()
 
@@ -953,6 +953,13 @@ class StagehandScheduler:
         res_entry.host_slab = None
 
     def _evict_block(self, block_id: str, save_back: bool = False) -> None:
+        """Evicts ``block_id`` and returns once its parameters' host values are final, as the
+        reference's synchronous eviction does (src/stagehand/scheduler.py:1184-1375). The eviction
+        loop uses :meth:`_evict_block_async`, which leaves the save-back copies running."""
+        self._evict_block_async(block_id, save_back=save_back)
+        self._sync_d2h_fences(block_id)
+
+    def _evict_block_async(self, block_id: str, save_back: bool = False) -> None:
         block_entry = self._registry.get(block_id)
         res_entry = self._residency.get_entry(block_id)
         module = block_entry.module_ref()
