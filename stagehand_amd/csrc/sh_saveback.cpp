@@ -23,6 +23,7 @@
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
 
+#include <atomic>
 #include <condition_variable>
 #include <cstdint>
 #include <deque>
@@ -67,7 +68,7 @@ struct sh_saveback {
   std::map<uint64_t, std::shared_ptr<Job>> jobs;   // every live ticket, in submission order
   uint64_t next_id = 1;
   bool stop = false;
-  bool timing = false;
+  std::atomic<bool> timing{false};  // read by the worker without the lock
   std::thread worker;
 };
 
@@ -100,7 +101,7 @@ void worker_loop(sh_saveback* sb) {
       fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), n);
       continue;
     }
-    if (sb->timing) hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &j->issue_ticks);
+    if (sb->timing.load()) hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &j->issue_ticks);
     hsa_signal_value_t issued = 0;
     for (const sh_copy_item& it : j->items) {
       hsa_status_t s = hsa_amd_memory_async_copy(it.dst, sb->cpu, it.src, sb->gpu, it.bytes, 0, nullptr, j->done);
@@ -303,8 +304,7 @@ extern "C" int sh_saveback_set_timing(sh_saveback* sb, int enable) {
   // the runtime-wide switch stays on once set: the HIP runtime's own copies may rely on it
   if (enable && hsa_amd_profiling_async_copy_enable(true) != HSA_STATUS_SUCCESS)
     return sh::fail(SH_ERR_HIP, "sh_saveback_set_timing: hsa_amd_profiling_async_copy_enable failed");
-  std::lock_guard<std::mutex> lk(sb->mu);
-  sb->timing = enable != 0;
+  sb->timing.store(enable != 0);
   return SH_OK;
 }
 
