@@ -214,3 +214,22 @@ def test_guards_see_outputs_only():
     sched2, _b, _t, _r, reg2, _p, _m = _stack(n=2, guards=g2)
     _run_step(sched2, reg2, 0, None)
     assert g2.seen == []
+
+
+def test_direct_eviction_waits_for_its_save_back_but_the_loop_does_not():
+    """``_evict_block`` returns with the block's host values final, as the reference's synchronous
+    eviction does (scheduler.py:1184-1375); the eviction loop leaves save-backs running."""
+    sched, budget, *_ = _stack(n=2, window=0, above=True)
+    calls = []
+    sched._evict_block_async = MagicMock(side_effect=lambda bid, save_back=False: calls.append(("evict", bid)))
+    sched._sync_d2h_fences = MagicMock(side_effect=lambda bid=None: calls.append(("sync", bid)))
+    sched._evict_block("block_0", save_back=True)
+    assert calls == [("evict", "block_0"), ("sync", "block_0")]
+    calls.clear()
+    fake = MagicMock(exec_order=0, size_bytes=1024, file_backed=False, squareq_backed=False)
+    sched._registry.get = MagicMock(return_value=fake)
+    sched._residency.eviction_candidates = MagicMock(return_value=[("block_1", MagicMock())])
+    sched._policy.score_for_eviction = MagicMock(return_value=1.0)
+    sched._budget.below_low_watermark = MagicMock(side_effect=[False, True])
+    sched._run_eviction()
+    assert calls == [("evict", "block_1")]
