@@ -38,14 +38,26 @@
 
 namespace {
 
+// A ticket's state. Its signal and fence belong to the object and are destroyed with it,
+// when the last reference drops: the queue's, the worker's, a waiter's snapshot or the
+// engine's map entry. Releasing a ticket therefore never frees a signal that a waiter on a
+// later ticket, or the worker, still holds.
 struct Job {
   uint64_t id = 0;
-  hipEvent_t fence = nullptr;
+  hipEvent_t fence = nullptr;  // none for a ticket without copies
   std::vector<sh_copy_item> items;
   hsa_signal_t done{0};
   int status = SH_OK;  // set (under the engine lock) before a failure completes `done`
   std::string error;
   uint64_t issue_ticks = 0;  // HSA system clock when the worker issued the first copy (timing only)
+
+  Job() = default;
+  Job(const Job&) = delete;
+  Job& operator=(const Job&) = delete;
+  ~Job() {
+    if (done.handle != 0) hsa_signal_destroy(done);
+    if (fence != nullptr) (void)hipEventDestroy(fence);
+  }
 };
 
 hsa_status_t find_cpu(hsa_agent_t agent, void* data) {
@@ -60,6 +72,7 @@ hsa_status_t find_cpu(hsa_agent_t agent, void* data) {
 }  // namespace
 
 struct sh_saveback {
+  sh::Live<sh::kLiveSaveback> live;
   int device = 0;
   hsa_agent_t cpu{0}, gpu{0};
   std::mutex mu;
@@ -85,6 +98,7 @@ void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, hsa_
 }
 
 void worker_loop(sh_saveback* sb) {
+  sh::name_thread("sh-saveback");
   (void)hipSetDevice(sb->device);
   for (;;) {
     std::shared_ptr<Job> j;
@@ -134,11 +148,6 @@ int jobs_upto(sh_saveback* sb, uint64_t ticket, std::vector<std::shared_ptr<Job>
   if (ticket == 0 || ticket >= sb->next_id) return sh::fail(SH_ERR_INVALID, "%s: unknown ticket %llu", who, (unsigned long long)ticket);
   for (auto it = sb->jobs.begin(); it != sb->jobs.end() && it->first <= ticket; ++it) out.push_back(it->second);
   return SH_OK;
-}
-
-void destroy_job(Job& j) {
-  if (j.done.handle != 0) hsa_signal_destroy(j.done);
-  if (j.fence != nullptr) (void)hipEventDestroy(j.fence);
 }
 
 }  // namespace
@@ -195,9 +204,8 @@ extern "C" int sh_saveback_destroy(sh_saveback* sb) {
   for (auto& kv : sb->jobs) {
     int st = wait_job(sb, kv.second);
     if (first == SH_OK) first = st;
-    destroy_job(*kv.second);
   }
-  sb->jobs.clear();
+  sb->jobs.clear();  // the last references: each job's signal and fence go with it
   delete sb;
   hsa_shut_down();
   return first;
@@ -216,25 +224,26 @@ extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, ui
       return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: item %llu has a NULL pointer", (unsigned long long)i);
     j->items.push_back(items[i]);
   }
-  if (hsa_signal_create((hsa_signal_value_t)j->items.size(), 0, nullptr, &j->done) != HSA_STATUS_SUCCESS)
+  if (hsa_signal_create((hsa_signal_value_t)j->items.size(), 0, nullptr, &j->done) != HSA_STATUS_SUCCESS) {
+    j->done.handle = 0;
     return sh::fail(SH_ERR_HIP, "sh_saveback_submit: hsa_signal_create failed");
-  hipError_t e = hipEventCreateWithFlags(&j->fence, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventRecord(j->fence, (hipStream_t)stream);
-  if (e != hipSuccess) {
-    destroy_job(*j);
-    return sh::fail(SH_ERR_HIP, "sh_saveback_submit: fence event: %s", hipGetErrorString(e));
+  }
+  // A ticket without copies is complete at once (its signal starts at 0): it gets no fence
+  // and never reaches the worker, which only waits for fences and issues copies.
+  const bool empty = j->items.empty();
+  if (!empty) {
+    hipError_t e = hipEventCreateWithFlags(&j->fence, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(j->fence, (hipStream_t)stream);
+    if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "sh_saveback_submit: fence event: %s", hipGetErrorString(e));
   }
   {
     std::lock_guard<std::mutex> lk(sb->mu);
-    if (sb->stop) {
-      destroy_job(*j);
-      return sh::fail(SH_ERR_STATE, "sh_saveback_submit: the engine is being destroyed");
-    }
+    if (sb->stop) return sh::fail(SH_ERR_STATE, "sh_saveback_submit: the engine is being destroyed");
     j->id = sb->next_id++;
     sb->jobs[j->id] = j;
-    sb->queue.push_back(j);
+    if (!empty) sb->queue.push_back(j);
   }
-  sb->cv.notify_one();
+  if (!empty) sb->cv.notify_one();
   *ticket = j->id;
   return SH_OK;
 }
@@ -280,12 +289,13 @@ extern "C" int sh_saveback_release(sh_saveback* sb, uint64_t ticket) {
     }
     j = it->second;
   }
-  int st = wait_job(sb, j);  // its own copies only: they read and write the caller's buffers
+  // Waits for its own copies only (they read and write the caller's buffers), then drops the
+  // map's reference. The signal and fence live on while the worker or a waiter holds the job.
+  int st = wait_job(sb, j);
   {
     std::lock_guard<std::mutex> lk(sb->mu);
     sb->jobs.erase(ticket);
   }
-  destroy_job(*j);
   return st;
 }
 

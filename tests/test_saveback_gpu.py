@@ -8,6 +8,8 @@ when a load reads what they wrote. Every case checks bytes bit for bit.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -180,5 +182,55 @@ def test_released_memory_is_counted_until_reaped_and_bounded(mode):
     assert eng.releasing_bytes() == 0
     for s, h in zip(srcs, homes):
         assert torch.equal(h, s.cpu())
+    eng.shutdown()
+    pool.shutdown()
+
+
+def test_release_of_earlier_tickets_while_a_later_one_is_waited_for():
+    """A waiter on a later ticket holds every earlier job it waits for; releasing those tickets
+    from another thread meanwhile drops only the engine's reference (the signals stay valid
+    until the waiter is done). Also: a ticket with no copies completes at once and may be
+    dropped before anything else happens."""
+    import threading
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    n = 24 << 20
+    srcs = [torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(8)]
+    dsts = [torch.zeros(n, dtype=torch.uint8, pin_memory=True) for _ in range(8)]
+    sb = SaveBackEngine(torch.cuda.current_device())
+    lib, h = _native.lib(), sb.handle
+    for rep in range(4):
+        a = torch.randn(2048, 2048, device="cuda")
+        for _ in range(8):  # the copies wait behind queued compute, so the waiter really waits
+            a = a @ a * 1e-3
+        tickets = [sb.submit(_items([(d, s)]), _stream()) for d, s in zip(dsts, srcs)]
+        result = {}
+
+        def waiter():
+            result["st"] = lib.sh_saveback_wait(h, ctypes.c_uint64(tickets[-1].ticket))
+
+        th = threading.Thread(target=waiter)
+        th.start()
+        for t in tickets[:-1]:
+            assert lib.sh_saveback_release(h, ctypes.c_uint64(t.ticket)) == _native.SH_OK
+        th.join(timeout=60)
+        assert not th.is_alive(), rep
+        assert result["st"] == _native.SH_OK, rep
+        for d, s in zip(dsts, srcs):
+            assert torch.equal(d, s.cpu()), rep
+        del tickets
+    sb.close()
+
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool, save_back="sdma")
+    empty_src = torch.empty(0, dtype=torch.uint8, device="cuda")
+    empty_dst = torch.empty(0, dtype=torch.uint8, pin_memory=True)
+    done = eng.d2h_into(empty_src, empty_dst)
+    assert isinstance(done, SaveBackTicket) and done.query()
+    del done  # released at once: no copy, no fence for the worker to wait on
+    later = eng.d2h_into(srcs[0], dsts[1])
+    later.synchronize()
+    assert torch.equal(dsts[1], srcs[0].cpu())
+    eng.drain()
     eng.shutdown()
     pool.shutdown()
