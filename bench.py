@@ -207,7 +207,7 @@ def cpu_reference_config4_step(seed: int) -> dict:
     import torch
 
     from oracle.torch_ref import host_dequant_into
-    from stagehand_amd.workloads import FluxStyleDiT, dit_linear_layers
+    from bench_workloads import FluxStyleDiT, dit_linear_layers
 
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
@@ -322,54 +322,6 @@ def _dit_inputs(seed: int, img_tokens: int = 4096, txt_tokens: int = 512, hidden
     return img, txt, vec
 
 
-def write_dit_squareq(model, path: Path, seed: int) -> dict:
-    """SquareQ v1 slab (torch.save payload) for every block Linear of ``model``:
-    int8 weights U{-127..127}, fp32 per-row scales exp(N(-6, 0.5)), zero points 0,
-    bf16 biases N(0, 0.02); generated on the device, written through host memory."""
-    import torch
-
-    from stagehand_amd.workloads import dit_linear_layers
-
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    layers, manifest = {}, []
-    for name, lin in dit_linear_layers(model):
-        o, i = lin.out_features, lin.in_features
-        q = torch.randint(-127, 128, (o, i), dtype=torch.int8, device="cuda", generator=g).cpu()
-        sc = torch.exp(torch.randn(o, device="cuda", generator=g) * 0.5 - 6.0).cpu()
-        b = (torch.randn(o, device="cuda", generator=g) * 0.02).to(torch.bfloat16).cpu()
-        layers[name] = {"qweight": q, "scale": sc, "zero_point": torch.zeros(o), "bias": b}
-        manifest.append({"name": name, "out": o, "inp": i, "padded_in": i, "has_bias": True})
-    torch.save({"manifest": {"layout": "rowwise_sym_int8", "layers": manifest}, "layers": layers}, str(path))
-    return {n: l for n, l in layers.items()}
-
-
-def write_dit_safetensors_sharded(model, directory: Path, seed: int) -> int:
-    """bf16 N(0, 0.02) weights, one safetensors shard per block + the index JSON."""
-    import torch
-    from safetensors.torch import save_file
-
-    directory.mkdir(parents=True, exist_ok=True)
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    weight_map, total = {}, 0
-    blocks = [(f"double_blocks.{i}", b) for i, b in enumerate(model.double_blocks)] + \
-             [(f"single_blocks.{i}", b) for i, b in enumerate(model.single_blocks)]
-    for bname, blk in blocks:
-        tensors = {}
-        for pname, prm in blk.named_parameters():
-            key = f"{bname}.{pname}"
-            if pname.endswith("norm.weight"):
-                tensors[key] = torch.ones(prm.shape, dtype=torch.bfloat16)
-            else:
-                tensors[key] = (torch.randn(prm.shape, device="cuda", generator=g) * 0.02).to(torch.bfloat16).cpu()
-            total += tensors[key].numel() * 2
-        shard = f"{bname}.safetensors"
-        save_file(tensors, str(directory / shard))
-        weight_map.update({k: shard for k in tensors})
-    (directory / "diffusion_pytorch_model.safetensors.index.json").write_text(
-        json.dumps({"metadata": {"total_size": total}, "weight_map": weight_map}))
-    return total
-
-
 def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
     import stagehand_amd as stagehand
 
@@ -397,7 +349,7 @@ def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
 def _dit_model():
     import torch
 
-    from stagehand_amd.workloads import FluxStyleDiT, materialize_norms_
+    from bench_workloads import FluxStyleDiT, materialize_norms_
 
     with torch.device("meta"):
         model = FluxStyleDiT()
@@ -472,7 +424,7 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     import torch
 
     import stagehand_amd as stagehand
-    from stagehand_amd.workloads import DIT_BLOCK_PATTERN, dit_forward_flops, dit_linear_layers
+    from bench_workloads import DIT_BLOCK_PATTERN, dit_forward_flops, dit_linear_layers
 
     model = _dit_model()  # a fresh module tree per runtime: conversion drops the module's weights
 
@@ -563,7 +515,7 @@ def _dit_host_bf16(seed: int):
     drawn on the device (fast), RMSNorm weights ones; frozen."""
     import torch
 
-    from stagehand_amd.workloads import FluxStyleDiT
+    from bench_workloads import FluxStyleDiT
 
     with torch.device("meta"):
         model = FluxStyleDiT()
@@ -589,7 +541,7 @@ def turbo_leg(args) -> dict:
     import torch
 
     from stagehand_amd.turbo import TurboConductor
-    from stagehand_amd.workloads import DIT_BLOCK_PATTERN, dit_forward_flops
+    from bench_workloads import DIT_BLOCK_PATTERN, dit_forward_flops
 
     img, txt, vec = _dit_inputs(args.seed)
     out = {"workload": "config3 bf16 Flux-style DiT (19 double + 38 single blocks, 11.84 B params), module-backed "
@@ -657,7 +609,7 @@ def train_leg(args) -> dict:
     import torch
 
     import stagehand_amd as stagehand
-    from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
+    from bench_workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
 
     g = torch.Generator(device="cuda").manual_seed(args.seed + 5)
     x = torch.randn(1, 4096, 4096, device="cuda", generator=g).to(torch.bfloat16)
@@ -753,7 +705,7 @@ def _vmm_run(args, src: Path) -> dict:
     import torch
 
     import stagehand_amd as stagehand
-    from stagehand_amd.workloads import DIT_BLOCK_PATTERN
+    from bench_workloads import DIT_BLOCK_PATTERN
 
     model = _dit_model()
     rt = stagehand.StagehandRuntime(model, _dit_config("file", args, False, args.file_reader), block_pattern=DIT_BLOCK_PATTERN,
@@ -880,7 +832,7 @@ def _first_steps(args, src: Path, reader: str, cold: bool, steps: int = 2, pinne
     import torch
 
     import stagehand_amd as stagehand
-    from stagehand_amd.workloads import DIT_BLOCK_PATTERN
+    from bench_workloads import DIT_BLOCK_PATTERN
 
     model = _dit_model()
     rt = stagehand.StagehandRuntime(model, _dit_config("file", args, pinned, reader), block_pattern=DIT_BLOCK_PATTERN,
@@ -970,6 +922,8 @@ def dit_leg(kind: str, args) -> dict:
 
     import torch
 
+    from bench_workloads import write_dit_safetensors_sharded, write_dit_squareq
+
     model = _dit_model()
     workdir = Path(tempfile.mkdtemp(prefix=f"sh_dit_{kind}_", dir=args.workdir))
     t0 = time.perf_counter()
@@ -1038,7 +992,7 @@ def profile_pass(args) -> int:
 
     from stagehand_amd.unpack import (KIND_COPY_BYTES, UnpackPlan, dequant_i8_rowscale_bf16, make_descs,
                                       unpack_cast_f32_bf16)
-    from stagehand_amd.workloads import config2_descs, config2_device_inputs, config2_regions
+    from bench_workloads import config2_descs, config2_device_inputs, config2_regions
 
     regions = config2_regions()
     n = sum(g.numel for g in regions)
@@ -1111,7 +1065,7 @@ def main() -> int:
     import torch
 
     from stagehand_amd.unpack import UnpackPlan, dequant_i8_rowscale_bf16, unpack_cast_f32_bf16
-    from stagehand_amd.workloads import config2_descs, config2_device_inputs, config2_regions
+    from bench_workloads import config2_descs, config2_device_inputs, config2_regions
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

@@ -1,5 +1,7 @@
 """Synthetic workloads of the benchmark configurations (seeded, no downloads).
 
+Used by ``bench.py`` and the tests; not part of the ``stagehand_amd`` package.
+
 ``config2_*`` builds the dequant/unpack microbenchmark: a packed slab of 128
 tensors cycling through 3072x3072, 3072x12288, 12288x3072, 3072x1 and 1000x77,
 int8 values uniform in [-127, 127], per-output-row fp32 scales
@@ -10,14 +12,17 @@ int8 regions after each 1000x77 tensor start 8 bytes off a 16-byte boundary.
 """
 from __future__ import annotations
 
+import json
 from dataclasses import dataclass
+from pathlib import Path
 
 import numpy as np
 import torch
 
 from stagehand_amd.unpack import KIND_F32_BF16, KIND_I8_ROWSCALE_BF16, make_descs
 
-__all__ = ["CONFIG2_SHAPES", "Region", "config2_regions", "config2_descs", "config2_device_inputs"]
+__all__ = ["CONFIG2_SHAPES", "Region", "config2_regions", "config2_descs", "config2_device_inputs", "FluxStyleDiT",
+           "TrainDiT", "write_dit_squareq", "write_dit_safetensors_sharded"]
 
 CONFIG2_SHAPES: tuple[tuple[int, int], ...] = ((3072, 3072), (3072, 12288), (12288, 3072), (3072, 1), (1000, 77))
 
@@ -304,3 +309,49 @@ def init_train_dit_(model: TrainDiT, seed: int, device: str = "cpu") -> TrainDiT
             trainable = isinstance(mod, LoRALinear)
             setattr(mod, name, _nn.Parameter(t, requires_grad=trainable))
     return model
+
+
+# ── weight files of the DiT configurations ──────────────────────────────────
+
+
+def write_dit_squareq(model, path: Path, seed: int) -> dict:
+    """SquareQ v1 slab (torch.save payload) for every block Linear of ``model``:
+    int8 weights U{-127..127}, fp32 per-row scales exp(N(-6, 0.5)), zero points 0,
+    bf16 biases N(0, 0.02); generated on the device, written through host memory."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    layers, manifest = {}, []
+    for name, lin in dit_linear_layers(model):
+        o, i = lin.out_features, lin.in_features
+        q = torch.randint(-127, 128, (o, i), dtype=torch.int8, device="cuda", generator=g).cpu()
+        sc = torch.exp(torch.randn(o, device="cuda", generator=g) * 0.5 - 6.0).cpu()
+        b = (torch.randn(o, device="cuda", generator=g) * 0.02).to(torch.bfloat16).cpu()
+        layers[name] = {"qweight": q, "scale": sc, "zero_point": torch.zeros(o), "bias": b}
+        manifest.append({"name": name, "out": o, "inp": i, "padded_in": i, "has_bias": True})
+    torch.save({"manifest": {"layout": "rowwise_sym_int8", "layers": manifest}, "layers": layers}, str(path))
+    return {n: l for n, l in layers.items()}
+
+
+def write_dit_safetensors_sharded(model, directory: Path, seed: int) -> int:
+    """bf16 N(0, 0.02) weights, one safetensors shard per block + the index JSON."""
+    from safetensors.torch import save_file
+
+    directory.mkdir(parents=True, exist_ok=True)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    weight_map, total = {}, 0
+    blocks = [(f"double_blocks.{i}", b) for i, b in enumerate(model.double_blocks)] + \
+             [(f"single_blocks.{i}", b) for i, b in enumerate(model.single_blocks)]
+    for bname, blk in blocks:
+        tensors = {}
+        for pname, prm in blk.named_parameters():
+            key = f"{bname}.{pname}"
+            if pname.endswith("norm.weight"):
+                tensors[key] = torch.ones(prm.shape, dtype=torch.bfloat16)
+            else:
+                tensors[key] = (torch.randn(prm.shape, device="cuda", generator=g) * 0.02).to(torch.bfloat16).cpu()
+            total += tensors[key].numel() * 2
+        shard = f"{bname}.safetensors"
+        save_file(tensors, str(directory / shard))
+        weight_map.update({k: shard for k in tensors})
+    (directory / "diffusion_pytorch_model.safetensors.index.json").write_text(
+        json.dumps({"metadata": {"total_size": total}, "weight_map": weight_map}))
+    return total

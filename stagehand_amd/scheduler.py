@@ -653,11 +653,11 @@ class StagehandScheduler:
 
     def _build_source(self, block_entry: BlockEntry, module: nn.Module, layout: Layout):
         if not self._has_cuda:
-            if block_entry.squareq_backed:
-                raise RuntimeError(
-                    f"block {block_entry.block_id!r} is SquareQ-backed: its dequantisation runs on the GPU only")
             slab = self._engine._pool.acquire(block_entry.size_bytes)
-            self._fill_file_backed_host(block_entry, module, layout, slab.buffer)
+            if block_entry.squareq_backed:
+                self._fill_squareq_host(block_entry, module, layout, slab.buffer)
+            else:
+                self._fill_file_backed_host(block_entry, module, layout, slab.buffer)
             return slab
         builder = SourceBuilder(block_entry.dtype, block_entry.size_bytes)
         if block_entry.squareq_backed:
@@ -719,14 +719,20 @@ class StagehandScheduler:
             else:
                 region.zero_()
 
-    def _add_squareq_regions(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, b: SourceBuilder) -> None:
-        """SquareQ-backed block: branch structure of src/stagehand/scheduler.py:243-325."""
+    def _squareq_actions(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, native_v2: bool):
+        """The branch walk of src/stagehand/scheduler.py:243-325 for a SquareQ-backed block.
+
+        Yields ``(offset, nbytes, dtype, action, payload)`` per layout entry in layout order:
+        ``"dequant"`` with ``(q2d[:out], in_flat, scale, zero_point)``; ``"param"`` with the host
+        tensor to cast into the region (a bias, or a module parameter / its cached copy);
+        ``"zero"``; or ``"v2file"`` with ``(path, spec, shape, numel)`` for a V2 tensor that the
+        native reader may take as file ranges (the caller falls back to the tensor branches by
+        sending the entry back with ``generator.send(False)``)."""
         params = dict(module.named_parameters())
         specs = {s.param_name: s for s in block_entry.squareq_param_specs}
         mutable = set(block_entry.module_param_names)
         path = str(block_entry.source_path)
         v2 = block_entry.source_format == "squareq_v2"
-        native = v2 and self._file_reader != "mmap"
         loaded: list[dict] = []
 
         def layers() -> dict[str, Any]:  # host views, only when a region needs them
@@ -738,8 +744,10 @@ class StagehandScheduler:
         for name, shape, dtype, offset, numel in layout:
             nbytes = numel * dtype.itemsize
             spec = specs.get(name)
-            if spec is not None and native and self._add_v2_file_region(b, path, spec, shape, numel, offset):
-                continue
+            if spec is not None and native_v2:
+                taken = yield offset, nbytes, dtype, "v2file", (path, spec, shape, numel)
+                if taken:
+                    continue
             if spec is not None:
                 layer = layers().get(spec.layer_name)
                 if isinstance(layer, dict):
@@ -750,31 +758,73 @@ class StagehandScheduler:
                             out_dim = int(shape[0]) if len(shape) else 0
                             in_flat = numel // max(out_dim, 1) if out_dim else 0
                             if len(shape) == 0 or out_dim <= 0 or in_flat <= 0:
-                                b.add_zero(offset, nbytes)
+                                yield offset, nbytes, dtype, "zero", None
                                 continue
                             q2d = q.reshape(int(q.shape[0]), -1)
                             sv, zv = s.reshape(-1), z.reshape(-1)
                             if sv[:out_dim].numel() != out_dim or zv[:out_dim].numel() != out_dim:
-                                b.add_zero(offset, nbytes)
+                                yield offset, nbytes, dtype, "zero", None
                                 continue
                             if q2d.shape[0] < out_dim or q2d.shape[1] < in_flat:
                                 raise ValueError(f"SquareQ layer {spec.layer_name!r}: qweight {tuple(q.shape)} "
                                                  f"is smaller than {out_dim}x{in_flat}")
-                            b.add_dequant(offset, q2d[:out_dim], in_flat, sv, zv)
+                            yield offset, nbytes, dtype, "dequant", (q2d[:out_dim], in_flat, sv, zv)
                             continue
                     elif spec.kind == "bias":
                         bias = layer.get("bias")
                         if isinstance(bias, torch.Tensor):
-                            b.add_param(offset, bias)
+                            yield offset, nbytes, dtype, "param", bias
                         else:
-                            b.add_zero(offset, nbytes)
+                            yield offset, nbytes, dtype, "zero", None
                         continue
             if name in mutable and name in params:
                 value = self._module_value(block_entry.block_id, params, name, numel, cache)
                 if value is not None:
-                    b.add_param(offset, _runtime_dtype_on_host(value, dtype), mutable=True)
+                    yield offset, nbytes, dtype, "module", value
                     continue
-            b.add_zero(offset, nbytes)
+            yield offset, nbytes, dtype, "zero", None
+
+    def _add_squareq_regions(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, b: SourceBuilder) -> None:
+        """SquareQ-backed block on the device: each branch becomes a region of the block source."""
+        native = block_entry.source_format == "squareq_v2" and self._file_reader != "mmap"
+        walk = self._squareq_actions(block_entry, module, layout, native)
+        item = next(walk, None)
+        while item is not None:
+            offset, nbytes, dtype, action, payload = item
+            reply = None
+            if action == "v2file":
+                reply = self._add_v2_file_region(b, *payload, offset)
+            elif action == "dequant":
+                q2d, in_flat, sv, zv = payload
+                b.add_dequant(offset, q2d, in_flat, sv, zv)
+            elif action == "param":
+                b.add_param(offset, payload)
+            elif action == "module":
+                b.add_param(offset, _runtime_dtype_on_host(payload, dtype), mutable=True)
+            else:
+                b.add_zero(offset, nbytes)
+            try:
+                item = walk.send(reply)
+            except StopIteration:
+                item = None
+
+    def _fill_squareq_host(self, block_entry: BlockEntry, module: nn.Module, layout: Layout, buffer: torch.Tensor) -> None:
+        """SquareQ-backed block without a GPU: the reference's host ops into the slab
+        (src/stagehand/scheduler.py:290-325) — ``(f32(q) - zp) * scale`` in two fp32 roundings,
+        then the cast to the runtime dtype, for each branch of the same walk."""
+        for offset, nbytes, dtype, action, payload in self._squareq_actions(block_entry, module, layout, False):
+            region = buffer[offset:offset + nbytes]
+            if action == "dequant":
+                q2d, in_flat, sv, zv = payload
+                out_dim = int(q2d.shape[0])
+                scale_vec = sv.to(dtype=torch.float32)[:out_dim]
+                zero_vec = zv.to(dtype=torch.float32)[:out_dim]
+                deq = (q2d[:, :in_flat].to(torch.float32) - zero_vec.unsqueeze(1)) * scale_vec.unsqueeze(1)
+                region.view(dtype).copy_(deq.to(dtype=dtype).reshape(-1))
+            elif action in ("param", "module"):
+                region.view(dtype).copy_(payload.detach().to(device="cpu", dtype=dtype).reshape(-1))
+            else:
+                region.zero_()
 
     def _add_v2_file_region(self, b: SourceBuilder, path: str, spec, shape, numel: int, offset: int) -> bool:
         """A SquareQ V2 weight or bias read by the native reader: the int8 rows, scales and zero
@@ -924,7 +974,7 @@ class StagehandScheduler:
         for _score, bid in scored:
             if self._budget.below_low_watermark():
                 break
-            self._evict_block_async(bid, save_back=not self._inference_mode)
+            self._evict_block(bid, save_back=not self._inference_mode, wait=False)
             self._telemetry.record_eviction()
             self._bound_save_back_backlog()
 
@@ -952,12 +1002,14 @@ class StagehandScheduler:
             self._engine._pool.release(res_entry.host_slab)
         res_entry.host_slab = None
 
-    def _evict_block(self, block_id: str, save_back: bool = False) -> None:
-        """Evicts ``block_id`` and returns once its parameters' host values are final, as the
-        reference's synchronous eviction does (src/stagehand/scheduler.py:1184-1375). The eviction
-        loop uses :meth:`_evict_block_async`, which leaves the save-back copies running."""
+    def _evict_block(self, block_id: str, save_back: bool = False, wait: bool = True) -> None:
+        """Evicts ``block_id`` (src/stagehand/scheduler.py:1184-1375). By default it returns once the
+        parameters' host values are final, as the reference's synchronous eviction does; the
+        eviction loop passes ``wait=False``, which leaves the save-back copies running (their
+        completion is waited for before anything reads what they wrote)."""
         self._evict_block_async(block_id, save_back=save_back)
-        self._sync_d2h_fences(block_id)
+        if wait:
+            self._sync_d2h_fences(block_id)
 
     def _evict_block_async(self, block_id: str, save_back: bool = False) -> None:
         block_entry = self._registry.get(block_id)

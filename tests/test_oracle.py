@@ -237,3 +237,48 @@ def test_stage_squareq_block_branches():
     assert not region["gone.weight"].any()  # missing layer, not module-backed → zero fill
     assert not region["nob.bias"].any()  # bias spec without bias → zero fill
     np.testing.assert_array_equal(region["evicted.weight"], oq.cast_f32_bf16(cache["evicted.weight"]))
+
+
+# ── oracle/torch_ref.py: the timed CPU baseline computes the checked values ─────
+
+def test_torch_ref_host_dequant_matches_golden_rows():
+    """``host_dequant_into`` (the reference's torch op sequence, scheduler.py:290-300, which the
+    bench times as the CPU baseline) writes the golden rows' bf16 patterns, at unaligned slab
+    offsets and with padded source rows."""
+    from oracle import torch_ref
+
+    z = _load("squareq_rows.npz")
+    cases = [(z[f"q{i}"], z[f"s{i}"], np.zeros_like(z[f"s{i}"]), z[f"out{i}"]) for i in range(5)]
+    cases.append((z["q_edge"], z["s_edge"], z["z_edge"], z["out_edge"]))
+    regions, off, want = [], 3, []
+    for q, s, zp, out in cases:
+        rows, cols = out.shape
+        padded = np.concatenate([q, np.full((rows, 5), 99, np.int8)], axis=1)  # padded_in columns are dropped
+        regions.append((off, torch.from_numpy(padded), torch.from_numpy(s), torch.from_numpy(zp), rows, cols))
+        want.append((off, out))
+        off += 2 * out.size + 6
+    slab = torch.full((off,), 0xA5, dtype=torch.uint8)
+    torch_ref.host_dequant_into(slab, regions)
+    raw = slab.numpy()
+    for o, out in want:
+        got = raw[o:o + 2 * out.size].view(np.uint16).reshape(out.shape)
+        assert np.array_equal(got, out)
+    assert (raw[:3] == 0xA5).all()  # nothing written outside the regions
+
+
+def test_torch_ref_host_cast_matches_golden_patterns():
+    """``host_cast_into`` (scheduler.py:181 / 1071) writes the golden bf16 patterns of every
+    non-NaN fp32 input, and agrees with ``cast_f32_bf16`` on a seeded config-2-like tensor."""
+    from oracle import torch_ref
+
+    z = _load("bf16_cast.npz")
+    f = z["f32_bits"].view(np.float32)
+    keep = ~np.isnan(f)
+    src = f[keep]
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((77, 1000)) * 0.02).astype(np.float32)
+    slab = torch.zeros(2 * (src.size + w.size) + 2, dtype=torch.uint8)
+    torch_ref.host_cast_into(slab, [(0, torch.from_numpy(src)), (2 * src.size + 2, torch.from_numpy(w))])
+    raw = slab.numpy()
+    assert np.array_equal(raw[:2 * src.size].view(np.uint16), z["bf16_bits"][keep])
+    assert np.array_equal(raw[2 * src.size + 2:].view(np.uint16), oq.cast_f32_bf16(w))

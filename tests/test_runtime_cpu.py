@@ -14,7 +14,7 @@ import torch
 
 import stagehand_amd as stagehand
 from stagehand_amd.residency import BlockState
-from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
+from bench_workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
 
 pytestmark = pytest.mark.skipif(torch.cuda.is_available(), reason="host-path runtime tests (no GPU)")
 

@@ -185,10 +185,12 @@ def test_save_back_rule(inference, want):
         sched._residency.eviction_candidates = MagicMock(return_value=[("block_0", MagicMock())])
         sched._policy.score_for_eviction = MagicMock(return_value=1.0)
         sched._budget.below_low_watermark = MagicMock(side_effect=[False, True])
-        sched._evict_block_async = MagicMock()  # the eviction loop leaves save-backs running
+        sched._evict_block = MagicMock()  # the reference's interception point (tests/test_scheduler.py:495-528)
         sched._run_eviction()
-        assert sched._evict_block_async.call_count == 1
-        assert sched._evict_block_async.call_args.kwargs["save_back"] is want
+        assert sched._evict_block.call_count == 1
+        _args, kwargs = sched._evict_block.call_args
+        assert kwargs["save_back"] is want
+        assert kwargs["wait"] is False  # the loop leaves save-backs running
 
 
 def test_inference_eviction_keeps_module_backed_values():

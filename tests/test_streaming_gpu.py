@@ -197,8 +197,8 @@ def test_dit_squareq_streaming_matches_unstreamed(tmp_path):
     from pathlib import Path as _P
 
     sys.path.insert(0, str(_P(__file__).resolve().parent.parent))
-    from bench import write_dit_squareq
-    from stagehand_amd.workloads import DIT_BLOCK_PATTERN, FluxStyleDiT, dit_linear_layers, materialize_norms_
+    from bench_workloads import write_dit_squareq
+    from bench_workloads import DIT_BLOCK_PATTERN, FluxStyleDiT, dit_linear_layers, materialize_norms_
 
     kw = dict(depth_double=2, depth_single=3, hidden=256, heads=2, mlp_ratio=4.0)
     with torch.device("meta"):
@@ -288,7 +288,7 @@ def test_pinned_source_images_refresh_mutable_params(tmp_path):
 
 
 def _train_dit(seed: int):
-    from stagehand_amd.workloads import TrainDiT, init_train_dit_
+    from bench_workloads import TrainDiT, init_train_dit_
 
     return init_train_dit_(TrainDiT(depth=4, hidden=128, heads=4, mlp_ratio=2.0, rank=8), seed)
 
@@ -301,7 +301,7 @@ def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back):
     updated LoRA weights match the same model trained unstreamed; with frozen host copies the
     frozen weights are not copied back at eviction. Save-backs on the SDMA engine and on the copy
     stream."""
-    from stagehand_amd.workloads import TRAIN_BLOCK_PATTERN
+    from bench_workloads import TRAIN_BLOCK_PATTERN
 
     model = _train_dit(5)
     ref = _train_dit(5).cuda()

@@ -27,7 +27,7 @@ from stagehand_amd.unpack import (
     make_descs,
     unpack_cast_f32_bf16,
 )
-from stagehand_amd.workloads import config2_descs, config2_device_inputs, config2_regions
+from bench_workloads import config2_descs, config2_device_inputs, config2_regions
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
