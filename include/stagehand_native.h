@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 3
+#define SH_ABI_VERSION 4
 
 enum sh_status {
   SH_OK = 0,
@@ -47,6 +47,20 @@ enum sh_status {
 const char* sh_last_error(void);
 /* SH_ABI_VERSION of the loaded library. */
 int sh_abi_version(void);
+
+/* Process teardown. The reference's native engines release their threads, streams and
+ * pinned memory in their Rust Drop impls when Python drops them (turbo_src/engine.rs:395-422,
+ * vmm_src/allocator.rs:648-713, the prefetch thread's join in vmm_src/prefetch.rs:22-46).
+ * Here each object's destroy call does that, and sh_shutdown ends what the library holds
+ * for the whole process: it joins the shared host copy threads (at once, or when a copy
+ * still running on another thread returns; they start again on the next use). It fills
+ * `live` (may be NULL) with the native objects not yet destroyed, so a caller at interpreter
+ * exit can check that nothing still runs when the HIP runtime is torn down. */
+typedef struct sh_live_counts {
+  uint64_t pools, loaders, savebacks, turbos, vmms, files;
+  uint64_t copy_threads; /* host copy threads still running */
+} sh_live_counts;
+int sh_shutdown(sh_live_counts* live);
 
 /* ───────────────────────── device, streams, events, copies ─────────────────────────
  * HIP rewrite of the CUDA runtime FFI the reference declares by hand in

@@ -12,8 +12,12 @@ weight-file reads, as the reference's open/mmap of a weight file raises).
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
+import itertools
+import logging
 import threading
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -22,6 +26,8 @@ from stagehand_amd.errors import StagehandOOMError
 
 __all__ = [
     "NativeLibraryError",
+    "track",
+    "shutdown",
     "lib",
     "check",
     "LIB_PATH",
@@ -108,6 +114,7 @@ _u32 = ctypes.c_uint32
 # name → argtypes; every function returns int status.
 _SIGNATURES: dict[str, list] = {
     "sh_abi_version": [],
+    "sh_shutdown": [_vp],
     "sh_device_count": [ctypes.POINTER(_i32)],
     "sh_set_device": [_i32],
     "sh_get_device": [ctypes.POINTER(_i32)],
@@ -237,7 +244,7 @@ VMM_REGION_DTYPE = np.dtype([("state", "<u4"), ("refcount", "<u4"), ("offset", "
 # Mirror of `struct sh_copy_item`.
 COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -301,3 +308,66 @@ def check(status: int, what: str = "") -> int:
 def call(name: str, *args) -> int:
     """Call native entry point *name* and raise on failure."""
     return check(getattr(lib(), name)(*args), name)
+
+
+# ── process teardown ─────────────────────────────────────────────────────────
+#
+# Native objects own threads (loader workers and advisors, save-back workers, the VMM
+# prefetch worker, the shared host copy threads), HIP streams, events and pinned memory.
+# Objects still open when the interpreter exits are closed by ``shutdown`` (registered
+# with atexit on first use), while the HIP runtime is still whole: users before what they
+# use — runtimes, then engines, then what engines hold — and sh_shutdown last.
+
+CLOSE_RUNTIME, CLOSE_ENGINE_USER, CLOSE_ENGINE, CLOSE_LEAF, CLOSE_POOL = range(5)
+
+log = logging.getLogger(__name__)
+
+
+class _LiveCounts(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint64) for name in
+                ("pools", "loaders", "savebacks", "turbos", "vmms", "files", "copy_threads")]
+
+
+_tracked: list[tuple[int, int, weakref.ref, str]] = []
+_tracked_lock = threading.Lock()
+_tracked_seq = itertools.count()
+_atexit_registered = False
+
+
+def track(obj: object, order: int, method: str = "close") -> None:
+    """Closes ``obj`` with ``obj.<method>()`` at interpreter exit if it is still alive then.
+    Objects close in ``order`` (CLOSE_RUNTIME first), the newest first within one order."""
+    global _atexit_registered
+    with _tracked_lock:
+        if len(_tracked) >= 1024:
+            _tracked[:] = [t for t in _tracked if t[2]() is not None]
+        _tracked.append((order, next(_tracked_seq), weakref.ref(obj), method))
+        if not _atexit_registered:
+            atexit.register(shutdown)
+            _atexit_registered = True
+
+
+def shutdown() -> dict[str, int]:
+    """Closes every tracked native object that is still alive, then ends the library's
+    process-wide state (``sh_shutdown``: the shared copy threads are joined). Returns the
+    native objects still alive afterwards, by kind (all zero when everything closed)."""
+    with _tracked_lock:
+        items = sorted(_tracked, key=lambda t: (t[0], -t[1]))
+        _tracked.clear()
+    for _order, _seq, ref, method in items:
+        obj = ref()
+        if obj is None:
+            continue
+        try:
+            getattr(obj, method)()
+        except Exception as exc:  # noqa: BLE001 — keep closing the rest
+            log.warning("stagehand shutdown: %s.%s() failed: %s", type(obj).__name__, method, exc)
+    if _lib is None:
+        return {}
+    counts = _LiveCounts()
+    check(_lib.sh_shutdown(ctypes.byref(counts)), "sh_shutdown")
+    out = {name: int(getattr(counts, name)) for name, _ in _LiveCounts._fields_}
+    left = {k: v for k, v in out.items() if v}
+    if left:
+        log.warning("stagehand shutdown: native objects still alive: %s", left)
+    return out

@@ -52,6 +52,7 @@
 #include "stagehand_native.h"
 
 struct sh_file {
+  sh::Live<sh::kLiveFile> live;
   int fd = -1;                    // buffered descriptor
   std::atomic<int> dfd{-1};       // O_DIRECT descriptor, -1 when unavailable
   int dfd_owned = -1;             // closed at sh_file_close even after a fallback

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -28,6 +29,22 @@ void clear_error();
       return ::sh::fail(SH_ERR_HIP, "HIP error %d (%s) in %s", (int)sh_e_,       \
                         hipGetErrorString(sh_e_), #call);                         \
   } while (0)
+
+// Live native objects by kind, for sh_shutdown's report. Each object struct holds a
+// Live<kind> member, so construction and destruction keep the count.
+enum LiveKind : int { kLivePool = 0, kLiveLoader, kLiveSaveback, kLiveTurbo, kLiveVmm, kLiveFile, kLiveKinds };
+extern std::atomic<int64_t> g_live[kLiveKinds];
+template <int K>
+struct Live {
+  Live() { g_live[K].fetch_add(1, std::memory_order_relaxed); }
+  ~Live() { g_live[K].fetch_sub(1, std::memory_order_relaxed); }
+  Live(const Live&) = delete;
+  Live& operator=(const Live&) = delete;
+};
+
+// Names the calling thread (at most 15 characters shown): every thread the library starts
+// is called "sh-<role>", so a process can tell them from the runtime's own threads.
+void name_thread(const char* name);
 
 // Runs fn(i) for every i in [0, n) on up to `threads` of the shared host copy
 // threads (the calling thread included); returns when all calls are done.

@@ -84,6 +84,7 @@ struct Ticket {
 }  // namespace
 
 struct sh_loader {
+  sh::Live<sh::kLiveLoader> live;
   sh_pool* pool = nullptr;
   uint64_t slab_bytes = 0;
   int device = 0;
@@ -330,6 +331,7 @@ void advise(sh_loader* L, Ticket& t) {
 }
 
 void worker_loop(sh_loader* L) {
+  sh::name_thread("sh-loader");
   for (;;) {
     uint64_t id = 0;
     Ticket* t = nullptr;
@@ -376,6 +378,7 @@ void worker_loop(sh_loader* L) {
 // while their files were known to be open; advice on a descriptor that has
 // since been closed or reused is at worst a wasted hint.
 void advisor_loop(sh_loader* L) {
+  sh::name_thread("sh-advisor");
   for (;;) {
     sh_loader::Advice a;
     {

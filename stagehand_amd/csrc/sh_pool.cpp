@@ -15,6 +15,7 @@
 // which releases the Python GIL for their duration.
 
 #include <hip/hip_runtime.h>
+#include <pthread.h>
 
 #include <algorithm>
 #include <atomic>
@@ -24,6 +25,7 @@
 #include <cstring>
 #include <deque>
 #include <functional>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <thread>
@@ -33,6 +35,7 @@
 #include "stagehand_native.h"
 
 struct sh_pool {
+  sh::Live<sh::kLivePool> live;
   uint8_t* base = nullptr;
   uint64_t slab_bytes = 0;
   uint32_t num_slabs = 0;
@@ -247,12 +250,33 @@ namespace {
 
 class CopyPool {
  public:
-  // Created on first use and intentionally never destroyed: joining worker
-  // threads from a static destructor at process exit races with the HIP
-  // runtime's and other libraries' own teardown.
-  static CopyPool& get() {
-    static CopyPool* inst = new CopyPool();
-    return *inst;
+  // The process-wide pool, created on first use. Without sh_shutdown it is never
+  // destroyed: a static destructor joining the threads at process exit would race
+  // with the HIP runtime's and other libraries' own teardown. sh_shutdown drops the
+  // global reference instead; the pool's threads are joined when the last user
+  // (sh_shutdown itself, or a parallel_for still running) lets go of it.
+  static std::shared_ptr<CopyPool> acquire() {
+    std::lock_guard<std::mutex> lk(global_mu());
+    std::shared_ptr<CopyPool>& inst = global();
+    if (!inst) inst.reset(new CopyPool());
+    return inst;
+  }
+  static std::shared_ptr<CopyPool> take_global() {
+    std::lock_guard<std::mutex> lk(global_mu());
+    std::shared_ptr<CopyPool> out;
+    out.swap(global());
+    return out;
+  }
+  static int64_t running_threads() { return running_.load(); }
+
+  ~CopyPool() {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (std::thread& t : workers_)
+      if (t.joinable()) t.join();
   }
 
   // Runs fn(i) for i in [0, n) on up to `threads` workers (caller included).
@@ -287,19 +311,26 @@ class CopyPool {
   CopyPool() {
     unsigned hw = std::thread::hardware_concurrency();
     unsigned n = std::max(1u, std::min(hw ? hw : 4u, 16u)) - 1;
-    for (unsigned i = 0; i < n; ++i) {
-      workers_.emplace_back([this, i] { loop(i); });
-      workers_.back().detach();
-    }
+    for (unsigned i = 0; i < n; ++i) workers_.emplace_back([this, i] { loop(i); });
+  }
+  static std::mutex& global_mu() {
+    static std::mutex* mu = new std::mutex();  // never destroyed (see acquire)
+    return *mu;
+  }
+  static std::shared_ptr<CopyPool>& global() {
+    static std::shared_ptr<CopyPool>* inst = new std::shared_ptr<CopyPool>();  // never destroyed
+    return *inst;
   }
   void loop(unsigned index) {
+    sh::name_thread("sh-copy");
+    running_.fetch_add(1);
     uint64_t seen = 0;
     for (;;) {
       std::function<void()> job;
       {
         std::unique_lock<std::mutex> lk(mu_);
         cv_.wait(lk, [&] { return stop_ || generation_ != seen; });
-        if (stop_) return;
+        if (stop_) break;
         seen = generation_;
         if (index >= active_ || !job_) continue;
         job = job_;
@@ -308,6 +339,7 @@ class CopyPool {
       std::lock_guard<std::mutex> lk(mu_);
       done_cv_.notify_all();
     }
+    running_.fetch_sub(1);
   }
 
   std::vector<std::thread> workers_;
@@ -317,14 +349,39 @@ class CopyPool {
   unsigned active_ = 0;
   uint64_t generation_ = 0;
   bool stop_ = false;
+  static std::atomic<int64_t> running_;
 };
+
+std::atomic<int64_t> CopyPool::running_{0};
 
 constexpr size_t kCopyPiece = 8u << 20;  // 8 MiB pieces spread over the workers
 
 }  // namespace
 
+std::atomic<int64_t> sh::g_live[sh::kLiveKinds];
+
+void sh::name_thread(const char* name) { (void)pthread_setname_np(pthread_self(), name); }
+
 void sh::parallel_for(size_t n, unsigned threads, const std::function<void(size_t)>& fn) {
-  CopyPool::get().parallel_for(n, threads, fn);
+  if (n == 0) return;
+  CopyPool::acquire()->parallel_for(n, threads, fn);
+}
+
+extern "C" int sh_shutdown(sh_live_counts* live) {
+  sh::clear_error();
+  // Dropping the global reference joins the copy threads here, or, when a parallel_for
+  // is still running on another thread, as soon as it returns.
+  CopyPool::take_global().reset();
+  if (live != nullptr) {
+    live->pools = (uint64_t)sh::g_live[sh::kLivePool].load();
+    live->loaders = (uint64_t)sh::g_live[sh::kLiveLoader].load();
+    live->savebacks = (uint64_t)sh::g_live[sh::kLiveSaveback].load();
+    live->turbos = (uint64_t)sh::g_live[sh::kLiveTurbo].load();
+    live->vmms = (uint64_t)sh::g_live[sh::kLiveVmm].load();
+    live->files = (uint64_t)sh::g_live[sh::kLiveFile].load();
+    live->copy_threads = (uint64_t)CopyPool::running_threads();
+  }
+  return SH_OK;
 }
 
 extern "C" int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threads) {
@@ -345,7 +402,7 @@ extern "C" int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threa
       pieces.push_back(p);
     }
   }
-  CopyPool::get().parallel_for(pieces.size(), threads > 0 ? (unsigned)threads : 1u, [&](size_t i) {
+  sh::parallel_for(pieces.size(), threads > 0 ? (unsigned)threads : 1u, [&](size_t i) {
     std::memcpy(pieces[i].dst, pieces[i].src, pieces[i].bytes);
   });
   return SH_OK;

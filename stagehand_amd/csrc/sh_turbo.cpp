@@ -67,6 +67,7 @@ struct Slot {
 }  // namespace
 
 struct sh_turbo {
+  sh::Live<sh::kLiveTurbo> live;
   std::mutex mu;
   std::vector<Block> blocks;
   std::vector<Slot> slots;

@@ -107,6 +107,8 @@ constexpr uint32_t unroll_of(uint32_t kind) {
                                                                                  : 1u;
 }
 constexpr uint32_t tile_of(uint32_t kind) { return kThreads * unroll_of(kind) * chunk_of(kind); }
+// Most tiles one plan may hold: a launch of n tiles has n * kThreads work-items, below 2^32.
+constexpr uint32_t kMaxTiles = 0xFFFFFFFFu / kThreads;
 
 // NB bytes as 32-bit words; loaded and stored with unaligned-capable 128-bit
 // (or 64-bit) vector memory operations.
@@ -531,8 +533,11 @@ int build_table(const sh_unpack_desc* descs, uint32_t n, std::vector<sh_unpack_d
     d.div_magic = sh::udiv_magic(d.cols);
     const uint64_t per_tile = tile_of(d.kind);
     const uint64_t nt = (numel + per_tile - 1) / per_tile;
-    if (tiles + nt > 0x7FFFFFFFull)
-      return sh::fail(SH_ERR_INVALID, "%s: plan needs more than 2^31-1 tiles", who);
+    // one workgroup of kThreads work-items per tile, in a 1-D grid: the launch must stay
+    // under 2^32 work-items
+    if (tiles + nt > kMaxTiles)
+      return sh::fail(SH_ERR_INVALID, "%s: plan needs more than %u tiles (%u work-items each); split it",
+                      who, kMaxTiles, kThreads);
     d.tile_begin = (uint32_t)tiles;
     d.ntiles = (uint32_t)nt;
     d.flags = 0;

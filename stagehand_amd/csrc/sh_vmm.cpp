@@ -73,6 +73,7 @@ struct VSlab {
 }  // namespace
 
 struct sh_vmm {
+  sh::Live<sh::kLiveVmm> live;
   int device = 0;
   size_t granularity = 0;
   hipMemAllocationProp prop{};
@@ -203,9 +204,12 @@ int evict_for_space(sh_vmm* v, uint64_t needed) {
     VRegion& r = *s.regions[c.r];
     if (r.refcount.load(std::memory_order_acquire) != 0) continue;
     uint8_t expect = kResident;
-    if (!r.state.compare_exchange_strong(expect, kUnmapped, std::memory_order_acq_rel)) continue;
-    // a fast-path ensure_resident increments before it re-checks the state
-    if (r.refcount.load(std::memory_order_acquire) != 0) {
+    // Claim, then re-check the refcount. A fast-path ensure_resident increments the refcount,
+    // then re-checks the state: each side stores one atomic and then loads the other, so both
+    // orders are seq_cst — with acquire/release alone both loads could miss the other's store
+    // and the region be unmapped under a handle.
+    if (!r.state.compare_exchange_strong(expect, kUnmapped, std::memory_order_seq_cst)) continue;
+    if (r.refcount.load(std::memory_order_seq_cst) != 0) {
       r.state.store(kResident, std::memory_order_release);
       continue;
     }
@@ -271,6 +275,7 @@ void prefetch_one(sh_vmm* v, uint32_t slab, uint32_t region) {
 }
 
 void worker_loop(sh_vmm* v) {
+  sh::name_thread("sh-vmm-prefetch");
   (void)hipSetDevice(v->device);
   for (;;) {
     std::pair<uint32_t, uint32_t> req;
@@ -407,8 +412,9 @@ extern "C" int sh_vmm_ensure_resident(sh_vmm* v, uint32_t slab, uint32_t region,
     if (region >= s->watermark.load(std::memory_order_acquire))
       return sh::fail(SH_ERR_WATERMARK, "Region watermarked — use fallback path");
     if (r->state.load(std::memory_order_acquire) == kResident) {
-      r->refcount.fetch_add(1, std::memory_order_acq_rel);
-      if (r->state.load(std::memory_order_acquire) == kResident) {
+      // seq_cst store-then-load, paired with the evictor's claim-then-recheck (evict_for_space)
+      r->refcount.fetch_add(1, std::memory_order_seq_cst);
+      if (r->state.load(std::memory_order_seq_cst) == kResident) {
         r->last_access.store(v->clock.fetch_add(1) + 1, std::memory_order_relaxed);
         *out = make_handle(v, slab, region, r->base, st, r->generation.load());
         return SH_OK;

@@ -44,6 +44,7 @@ class WeightFile:
         flags = _native.SH_FILE_DIRECT if direct else 0
         _native.call("sh_file_open", self.path.encode(), flags, ctypes.byref(h))
         self._h: int | None = h.value
+        _native.track(self, _native.CLOSE_LEAF)
         self.size = self.info()["size"]
 
     @property

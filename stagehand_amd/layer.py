@@ -20,6 +20,7 @@ import math
 import torch
 from torch import nn
 
+from stagehand_amd import _native
 from stagehand_amd.budget import BudgetManager
 from stagehand_amd.config import StagehandConfig
 from stagehand_amd.guards import NumericGuard
@@ -154,6 +155,7 @@ class LayerRuntime:
         self._hook_handles: list = []
         self._mode = "trace"
         self._install_hooks(self._registry_order(), trace=True)
+        _native.track(self, _native.CLOSE_RUNTIME, "shutdown")
         log.info("LayerRuntime: %d layers discovered, pool=%dMB (%dMB slabs), prefetch_k=%d, mode=trace",
                  len(layers), self._config.pinned_pool_mb, self._config.pinned_slab_mb, prefetch_k)
 

@@ -68,6 +68,7 @@ class PinnedPool:
         _native.call("sh_pool_create", self._num_slabs, self._slab_bytes, int(use_pin), ctypes.byref(handle))
         self._handle = handle
         self._pinned = use_pin
+        _native.track(self, _native.CLOSE_POOL, "shutdown")
         self._slabs: list[PinnedSlab] = []
         for i in range(self._num_slabs):
             ptr = ctypes.c_void_p()

@@ -21,6 +21,7 @@ from typing import Generator
 import torch
 from torch import nn
 
+from stagehand_amd import _native
 from stagehand_amd.budget import BudgetManager
 from stagehand_amd.config import StagehandConfig
 from stagehand_amd.guards import NumericGuard
@@ -103,6 +104,8 @@ class StagehandRuntime:
                 except Exception as e:  # noqa: BLE001 — the block-swap path still works
                     log.warning("VMM init failed, using block-swap: %s", e)
                     self._vmm = None
+        self._shut_down = False
+        _native.track(self, _native.CLOSE_RUNTIME, "shutdown")
         log.info("StagehandRuntime: %d blocks registered, pool=%dMB, inference=%s", len(self._registry),
                  config.pinned_pool_mb, inference_mode)
 
@@ -335,6 +338,9 @@ class StagehandRuntime:
     # ── shutdown ─────────────────────────────────────────────────────
 
     def shutdown(self) -> None:
+        if self._shut_down:
+            return
+        self._shut_down = True
         if _DEBUG_SHUTDOWN:
             print("[stagehand/debug] runtime.shutdown: engine drain start", flush=True)
         if self._vmm is not None:
@@ -348,6 +354,7 @@ class StagehandRuntime:
         self._telemetry.close()
 
     def shutdown_keep_pool(self) -> PinnedPool:
+        self._shut_down = True
         self._engine.shutdown()
         self._scheduler.close()
         self._telemetry.close()

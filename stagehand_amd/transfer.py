@@ -21,13 +21,11 @@ submission, as in the reference (src/stagehand/transfer.py:136-138).
 """
 from __future__ import annotations
 
-import atexit
 import ctypes
 import logging
 import os
 import threading
 import time
-import weakref
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any
 
@@ -100,7 +98,7 @@ class SaveBackEngine:
         _native.call("sh_saveback_create", int(device), ctypes.byref(h))
         self._h: ctypes.c_void_p | None = h
         self._timing = False
-        _LIVE_SAVEBACKS.add(self)
+        _native.track(self, _native.CLOSE_LEAF)
 
     @property
     def handle(self) -> ctypes.c_void_p:
@@ -133,26 +131,11 @@ class SaveBackEngine:
     def close(self) -> None:
         if self._h is not None:
             h, self._h = self._h, None
-            _LIVE_SAVEBACKS.discard(self)
             _native.call("sh_saveback_destroy", h)
 
     def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
         try:
             self.close()
-        except Exception:
-            pass
-
-
-# Engines still open at interpreter exit are closed before the HIP runtime goes away
-# (their worker thread waits for HIP events).
-_LIVE_SAVEBACKS: "weakref.WeakSet[SaveBackEngine]" = weakref.WeakSet()
-
-
-@atexit.register
-def _close_savebacks() -> None:
-    for sb in list(_LIVE_SAVEBACKS):
-        try:
-            sb.close()
         except Exception:
             pass
 
@@ -279,6 +262,7 @@ class AsyncTransferEngine:
         self._trace_ref: NativeEvent | None = None
         self._trace_loads: list[tuple[str, int, float, float, float]] = []
         self._trace_compute: list[tuple[str, NativeEvent, NativeEvent]] = []
+        _native.track(self, _native.CLOSE_ENGINE, "shutdown")
         if self._has_cuda:
             _native.call("sh_set_device", torch.cuda.current_device())
             if copy_stream is not None:

@@ -60,6 +60,7 @@ class TransferEngine:
         h = ctypes.c_void_p()
         _native.call("sh_turbo_create", ctypes.byref(h))
         self._h = h
+        _native.track(self, _native.CLOSE_ENGINE)
 
     def _handle(self) -> ctypes.c_void_p:
         if self._h is None:

@@ -88,6 +88,7 @@ class UnpackPlan:
         handle = ctypes.c_void_p()
         _native.call("sh_plan_create", table.ctypes.data, len(table), ctypes.byref(handle))
         self._handle = handle
+        _native.track(self, _native.CLOSE_LEAF)
         info = np.zeros(1, dtype=PLAN_INFO_DTYPE)
         _native.call("sh_plan_get_info", handle, info.ctypes.data)
         self.info = {name: int(info[0][name]) for name in PLAN_INFO_DTYPE.names}

@@ -93,6 +93,7 @@ class SlabAllocator:
         _native.call("sh_vmm_create", int(device), 0 if ceiling_mb is None else int(ceiling_mb) << 20, ctypes.byref(h))
         self._h = h
         self.device = int(device)
+        _native.track(self, _native.CLOSE_ENGINE)
 
     def _handle(self) -> ctypes.c_void_p:
         if self._h is None:
@@ -523,6 +524,7 @@ class VmmManager:
         self._priority_counter = 0
         self._engine = engine
         self._file_reader = file_reader
+        _native.track(self, _native.CLOSE_ENGINE_USER, "shutdown")
         s = self.allocator.stats()
         log.info("VMM: allocator ready. ceiling=%.2fGB, granularity=%.1fMB", s["vram_ceiling"] / 1e9,
                  s["granularity"] / 1e6)

@@ -182,3 +182,17 @@ def test_index_division_is_exact():
 def test_index_division_rejects_zero():
     with pytest.raises(ValueError):
         _div(0, np.array([1], np.uint32))
+
+
+def test_plan_describe_refuses_plans_beyond_the_launch_limit():
+    """A plan launches one workgroup of SH_UNPACK_THREADS (512) work-items per tile in a 1-D grid,
+    which must stay under 2^32 work-items: the largest plan has (2^32 - 1) // 512 tiles, and one
+    tile more is refused at validation instead of failing at launch."""
+    max_tiles = (2**32 - 1) // 512
+    per_tile = (1 << 20) // describe([(KIND_F32_BF16, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
+    info = describe([(KIND_F32_BF16, 0, 0, max_tiles, per_tile, 0, 0)])
+    assert info["n_tiles"] == max_tiles
+    table = make_descs([(KIND_F32_BF16, 0, 0, max_tiles + 1, per_tile, 0, 0)])
+    out = np.zeros(1, dtype=PLAN_INFO_DTYPE)
+    assert _native.lib().sh_plan_describe(table.ctypes.data, len(table), out.ctypes.data) == _native.SH_ERR_INVALID
+    assert b"tiles" in _native.lib().sh_last_error()
