@@ -198,6 +198,26 @@ int sh_unpack_cast_f32_bf16(const sh_plan* plan,
                             const float* src, size_t src_bytes,
                             uint16_t* dst, size_t dst_bytes, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory — code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. It does what
+ * sh_plan_create + sh_unpack + sh_plan_destroy do for `descs`, with the same kernels and the
+ * same results, but the plan's launch table and tile map go into a library-owned static
+ * device array of SH_UNPACK_NOALLOC_SCRATCH_BYTES (8 MiB) on each GPU it runs on, held until
+ * the process ends; it calls no device allocator. Descriptors reach the device as kernel
+ * arguments, so nothing on the host has to outlive the call. Limits: at most
+ * SH_UNPACK_NOALLOC_MAX_DESCS descriptors after the plan's splitting of oversize regions and
+ * SH_UNPACK_NOALLOC_MAX_TILES tiles (config 2's dequant needs 270k, its cast 1.08 M);
+ * beyond them it returns SH_ERR_INVALID. All calls on one GPU share its array and leave the
+ * last call's table in it: calls ordered on one stream are safe, calls that overlap on one
+ * GPU (other streams, other threads) race. */
+#define SH_UNPACK_NOALLOC_MAX_DESCS 2048u
+#define SH_UNPACK_NOALLOC_MAX_TILES 2064384u
+#define SH_UNPACK_NOALLOC_SCRATCH_BYTES (8u << 20)
+int sh_unpack_noalloc(const sh_unpack_desc* descs, uint32_t n,
+                      const void* src, size_t src_bytes,
+                      const float* scales, const float* zero_points, size_t n_scale,
+                      void* dst, size_t dst_bytes, void* stream);
+
 /* ───────────────────────── pinned slab pool ─────────────────────────
  * Replaces the torch pinned-tensor pool of src/stagehand/pool.py:42-246
  * (PinnedPool.__init__ :58-116, acquire :122-175, release :181-196,

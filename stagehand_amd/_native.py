@@ -114,6 +114,7 @@ _u32 = ctypes.c_uint32
 # name → argtypes; every function returns int status.
 _SIGNATURES: dict[str, list] = {
     "sh_abi_version": [],
+    "sh_unpack_noalloc": [_vp, _u32, _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp],
     "sh_shutdown": [_vp],
     "sh_device_count": [ctypes.POINTER(_i32)],
     "sh_set_device": [_i32],

@@ -37,6 +37,7 @@
 #include <cstdint>
 #include <cstring>
 #include <new>
+#include <mutex>
 #include <vector>
 
 #include "sh_internal.h"
@@ -477,6 +478,47 @@ extern "C" __global__ __launch_bounds__(kThreads) void sh_unpack_mixed_zp_kernel
   unpack_body<kMaskAll, true>(descs, tile_map, src, scales, zps, dst);
 }
 
+// ── allocation-free launches (sh_unpack_noalloc) ─────────────────────────────
+//
+// The launch table and the tile map of a call live in this file-scope array, one copy per
+// GPU, held until the process ends: descriptors at offset 0, the tile map after them. In
+// host code `scratch` is only a stand-in for the symbol; the device address comes from
+// hipGetSymbolAddress (scratch_on_current_device below).
+static_assert(SH_UNPACK_NOALLOC_SCRATCH_BYTES ==
+                  SH_UNPACK_NOALLOC_MAX_DESCS * sizeof(sh_unpack_desc) + SH_UNPACK_NOALLOC_MAX_TILES * 4ull,
+              "scratch layout: descriptor table, then one uint32 per tile");
+static __device__ __align__(256) uint8_t scratch[SH_UNPACK_NOALLOC_SCRATCH_BYTES];
+
+// Descriptors travel to the device as kernel arguments, in chunks: no host buffer has to
+// outlive the call and no copy is queued from pageable memory.
+constexpr uint32_t kDescChunk = 32;  // 2 KiB of descriptors per launch's arguments
+struct DescChunk {
+  sh_unpack_desc d[kDescChunk];
+  uint32_t first;
+  uint32_t count;
+};
+
+extern "C" __global__ __launch_bounds__(kDescChunk) void sh_put_descs_kernel(DescChunk c, sh_unpack_desc* table) {
+  if (threadIdx.x < c.count) table[c.first + threadIdx.x] = c.d[threadIdx.x];
+}
+
+// map[t] = the descriptor whose tiles [tile_begin, tile_begin + ntiles) hold t. Descriptors
+// hold consecutive, non-empty tile ranges in table order, so a binary search over tile_begin
+// finds it.
+extern "C" __global__ __launch_bounds__(256) void sh_fill_tile_map_kernel(const sh_unpack_desc* __restrict__ table,
+                                                                          uint32_t n, uint32_t* __restrict__ map,
+                                                                          uint32_t n_tiles) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= n_tiles) return;
+  uint32_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (table[mid].tile_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  map[t] = lo;
+}
+
 namespace {
 
 // ── host side: plans ──────────────────────────────────────────────────────
@@ -680,6 +722,43 @@ extern "C" int sh_plan_get_info(const sh_plan* plan, sh_plan_info* info) {
 
 namespace {
 
+// Checks the caller's buffers against a plan's extents (SH_OK or SH_ERR_INVALID).
+int check_buffers(const sh_plan_info& in, const void* src, size_t src_bytes, const float* scales, size_t n_scale,
+                  const void* dst, size_t dst_bytes, const char* who) {
+  if (in.src_extent > 0 && (src == nullptr || src_bytes < in.src_extent))
+    return sh::fail(SH_ERR_INVALID, "%s: source buffer of %zu bytes is smaller than the plan's %llu", who,
+                    src == nullptr ? (size_t)0 : src_bytes, (unsigned long long)in.src_extent);
+  if (dst == nullptr || dst_bytes < in.dst_extent)
+    return sh::fail(SH_ERR_INVALID, "%s: destination buffer of %zu bytes is smaller than the plan's %llu", who,
+                    dst == nullptr ? (size_t)0 : dst_bytes, (unsigned long long)in.dst_extent);
+  const bool has_i8 = (in.kind_mask & (bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROWSCALE_F32))) != 0;
+  if (has_i8 && (scales == nullptr || n_scale < in.scale_extent))
+    return sh::fail(SH_ERR_INVALID, "%s: %zu scales given, the plan reads %llu", who,
+                    scales == nullptr ? (size_t)0 : n_scale, (unsigned long long)in.scale_extent);
+  return SH_OK;
+}
+
+// Launches the unpack kernel for a checked plan whose table and tile map are at d_descs /
+// d_tile_map on the current device.
+int launch_tiles(const sh_plan_info& in, const sh_unpack_desc* d_descs, const uint32_t* d_tile_map,
+                 const void* src, const float* scales, const float* zps, void* dst, void* stream) {
+  const bool has_i8 = (in.kind_mask & (bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROWSCALE_F32))) != 0;
+  const bool has_zp = has_i8 && zps != nullptr;
+
+  void (*kern)(SH_KERNEL_ARGS);
+  if (in.kind_mask == kMaskDequantBf16)
+    kern = has_zp ? sh_dequant_i8_bf16_zp_kernel : sh_dequant_i8_bf16_kernel;
+  else if (in.kind_mask == kMaskCastBf16)
+    kern = sh_cast_f32_bf16_kernel;
+  else
+    kern = has_zp ? sh_unpack_mixed_zp_kernel : sh_unpack_mixed_kernel;
+
+  hipLaunchKernelGGL(kern, dim3(in.n_tiles), dim3(kThreads), 0, (hipStream_t)stream, d_descs, d_tile_map,
+                     (const uint8_t*)src, scales, has_zp ? zps : nullptr, (uint8_t*)dst);
+  SH_HIP(hipGetLastError());
+  return SH_OK;
+}
+
 int launch(const sh_plan* plan, const void* src, size_t src_bytes, const float* scales,
            const float* zps, size_t n_scale, void* dst, size_t dst_bytes, void* stream,
            uint32_t required_mask, const char* who) {
@@ -695,29 +774,29 @@ int launch(const sh_plan* plan, const void* src, size_t src_bytes, const float* 
   if (cur != plan->device)
     return sh::fail(SH_ERR_INVALID, "%s: plan was built on device %d but device %d is current", who,
                     plan->device, cur);
-  if (in.src_extent > 0 && (src == nullptr || src_bytes < in.src_extent))
-    return sh::fail(SH_ERR_INVALID, "%s: source buffer of %zu bytes is smaller than the plan's %llu", who,
-                    src == nullptr ? (size_t)0 : src_bytes, (unsigned long long)in.src_extent);
-  if (dst == nullptr || dst_bytes < in.dst_extent)
-    return sh::fail(SH_ERR_INVALID, "%s: destination buffer of %zu bytes is smaller than the plan's %llu", who,
-                    dst == nullptr ? (size_t)0 : dst_bytes, (unsigned long long)in.dst_extent);
-  const bool has_i8 = (in.kind_mask & (bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROWSCALE_F32))) != 0;
-  if (has_i8 && (scales == nullptr || n_scale < in.scale_extent))
-    return sh::fail(SH_ERR_INVALID, "%s: %zu scales given, the plan reads %llu", who,
-                    scales == nullptr ? (size_t)0 : n_scale, (unsigned long long)in.scale_extent);
-  const bool has_zp = has_i8 && zps != nullptr;
+  if (int st = check_buffers(in, src, src_bytes, scales, n_scale, dst, dst_bytes, who)) return st;
+  return launch_tiles(in, plan->d_descs, plan->d_tile_map, src, scales, zps, dst, stream);
+}
 
-  void (*kern)(SH_KERNEL_ARGS);
-  if (in.kind_mask == kMaskDequantBf16)
-    kern = has_zp ? sh_dequant_i8_bf16_zp_kernel : sh_dequant_i8_bf16_kernel;
-  else if (in.kind_mask == kMaskCastBf16)
-    kern = sh_cast_f32_bf16_kernel;
-  else
-    kern = has_zp ? sh_unpack_mixed_zp_kernel : sh_unpack_mixed_kernel;
+// The scratch array's device address on the current device, looked up once per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
-  hipLaunchKernelGGL(kern, dim3(in.n_tiles), dim3(kThreads), 0, (hipStream_t)stream, plan->d_descs,
-                     plan->d_tile_map, (const uint8_t*)src, scales, has_zp ? zps : nullptr, (uint8_t*)dst);
-  SH_HIP(hipGetLastError());
+int scratch_on_current_device(void** out, const char* who) {
+  int dev = -1;
+  SH_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return sh::fail(SH_ERR_INVALID, "%s: device %d out of range", who, dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return sh::fail(SH_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                      hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return SH_OK;
 }
 
@@ -740,6 +819,41 @@ extern "C" int sh_unpack_cast_f32_bf16(const sh_plan* plan, const float* src, si
                                        size_t dst_bytes, void* stream) {
   return launch(plan, src, src_bytes, nullptr, nullptr, 0, dst, dst_bytes, stream, kMaskCastBf16,
                 "sh_unpack_cast_f32_bf16");
+}
+
+extern "C" int sh_unpack_noalloc(const sh_unpack_desc* descs, uint32_t n, const void* src, size_t src_bytes,
+                                 const float* scales, const float* zero_points, size_t n_scale, void* dst,
+                                 size_t dst_bytes, void* stream) {
+  static const char* who = "sh_unpack_noalloc";
+  sh::clear_error();
+  thread_local std::vector<sh_unpack_desc> table;  // host side only, reused across calls
+  sh_plan_info in{};
+  if (int st = build_table(descs, n, table, in, who)) return st;
+  if (table.size() > SH_UNPACK_NOALLOC_MAX_DESCS)
+    return sh::fail(SH_ERR_INVALID, "%s: the plan needs %zu descriptors after splitting; at most %u fit the scratch",
+                    who, table.size(), (unsigned)SH_UNPACK_NOALLOC_MAX_DESCS);
+  if (in.n_tiles > SH_UNPACK_NOALLOC_MAX_TILES)
+    return sh::fail(SH_ERR_INVALID, "%s: the plan needs %u tiles; at most %u fit the scratch", who, in.n_tiles,
+                    (unsigned)SH_UNPACK_NOALLOC_MAX_TILES);
+  if (in.n_tiles == 0) return SH_OK;
+  if (int st = check_buffers(in, src, src_bytes, scales, n_scale, dst, dst_bytes, who)) return st;
+  void* base = nullptr;
+  if (int st = scratch_on_current_device(&base, who)) return st;
+  sh_unpack_desc* d_descs = (sh_unpack_desc*)base;
+  uint32_t* d_map = (uint32_t*)((uint8_t*)base + SH_UNPACK_NOALLOC_MAX_DESCS * sizeof(sh_unpack_desc));
+  const hipStream_t s = (hipStream_t)stream;
+  const uint32_t nd = (uint32_t)table.size();
+  for (uint32_t first = 0; first < nd; first += kDescChunk) {
+    DescChunk c{};
+    c.first = first;
+    c.count = std::min(kDescChunk, nd - first);
+    std::copy(table.begin() + first, table.begin() + first + c.count, c.d);
+    hipLaunchKernelGGL(sh_put_descs_kernel, dim3(1), dim3(kDescChunk), 0, s, c, d_descs);
+  }
+  hipLaunchKernelGGL(sh_fill_tile_map_kernel, dim3((in.n_tiles + 255) / 256), dim3(256), 0, s,
+                     (const sh_unpack_desc*)d_descs, nd, d_map, in.n_tiles);
+  SH_HIP(hipGetLastError());
+  return launch_tiles(in, d_descs, d_map, src, scales, zero_points, dst, stream);
 }
 
 extern "C" int sh_index_div(uint32_t d, const uint32_t* n, uint32_t* q, size_t count) {

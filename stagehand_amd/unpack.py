@@ -35,6 +35,7 @@ __all__ = [
     "make_descs",
     "dequant_i8_rowscale_bf16",
     "unpack_cast_f32_bf16",
+    "unpack_noalloc",
     "KIND_I8_ROWSCALE_BF16",
     "KIND_I8_ROWSCALE_F32",
     "KIND_F32_BF16",
@@ -162,3 +163,32 @@ def unpack_cast_f32_bf16(
 ) -> None:
     """fp32→bf16 unpack of every region of ``plan`` (all SH_KIND_F32_BF16)."""
     plan.run(src, dst, None, None, stream, entry="sh_unpack_cast_f32_bf16")
+
+
+def unpack_noalloc(
+    descs: np.ndarray,
+    src: torch.Tensor | None,
+    dst: torch.Tensor,
+    scales: torch.Tensor | None = None,
+    zero_points: torch.Tensor | None = None,
+    stream: torch.cuda.Stream | int | None = None,
+) -> None:
+    """``dst`` ← unpack(``src``) for the descriptor table ``descs``, allocating no device memory
+    (``sh_unpack_noalloc``: the launch table lives in the library's static per-GPU scratch).
+
+    The results equal an :class:`UnpackPlan` of the same table run with ``sh_unpack``. Calls on one
+    GPU share the scratch: calls ordered on one stream are safe, overlapping calls race."""
+    table = np.ascontiguousarray(descs, dtype=DESC_DTYPE)
+    sp, sb = _device_ptr(src, "src")
+    dp, db = _device_ptr(dst, "dst")
+    if scales is not None and scales.dtype != torch.float32:
+        raise ValueError("scales must be float32")
+    if zero_points is not None and zero_points.dtype != torch.float32:
+        raise ValueError("zero_points must be float32")
+    cp, cb = _device_ptr(scales, "scales")
+    zp, zb = _device_ptr(zero_points, "zero_points")
+    n_scale = cb // 4
+    if zero_points is not None and zb // 4 < n_scale:
+        raise ValueError("zero_points must hold as many entries as scales")
+    _native.call("sh_unpack_noalloc", table.ctypes.data if len(table) else None, len(table), sp or None, sb,
+                 cp or None, zp or None, n_scale, dp, db, _stream_handle(stream))

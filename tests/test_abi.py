@@ -196,3 +196,21 @@ def test_plan_describe_refuses_plans_beyond_the_launch_limit():
     out = np.zeros(1, dtype=PLAN_INFO_DTYPE)
     assert _native.lib().sh_plan_describe(table.ctypes.data, len(table), out.ctypes.data) == _native.SH_ERR_INVALID
     assert b"tiles" in _native.lib().sh_last_error()
+
+
+def test_noalloc_entry_point_refuses_tables_beyond_its_scratch():
+    """``sh_unpack_noalloc`` checks its static scratch's limits on the host, before any device call:
+    at most SH_UNPACK_NOALLOC_MAX_DESCS descriptors and SH_UNPACK_NOALLOC_MAX_TILES tiles."""
+    header = (Path(__file__).resolve().parent.parent / "include" / "stagehand_native.h").read_text()
+    max_descs = int(re.search(r"#define SH_UNPACK_NOALLOC_MAX_DESCS (\d+)u", header).group(1))
+    max_tiles = int(re.search(r"#define SH_UNPACK_NOALLOC_MAX_TILES (\d+)u", header).group(1))
+    assert max_descs * 64 + max_tiles * 4 == 8 << 20  # the scratch: table, then one uint32 per tile
+    lib = _native.lib()
+    per_tile = (1 << 20) // describe([(KIND_F32_BF16, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
+    tiles = make_descs([(KIND_F32_BF16, 0, 0, max_tiles + 1, per_tile, 0, 0)])
+    assert lib.sh_unpack_noalloc(tiles.ctypes.data, 1, None, 0, None, None, 0, None, 0, None) == _native.SH_ERR_INVALID
+    assert b"tiles" in lib.sh_last_error()
+    many = make_descs([(KIND_ZERO_BYTES, 0, 16 * i, 1, 16, 0, 0) for i in range(max_descs + 1)])
+    assert lib.sh_unpack_noalloc(many.ctypes.data, len(many), None, 0, None, None, 0, None, 0,
+                                 None) == _native.SH_ERR_INVALID
+    assert b"descriptors" in lib.sh_last_error()
