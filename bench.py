@@ -153,13 +153,45 @@ def copy_kernel_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
     return reps * 2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9
 
 
+def host_cores() -> dict:
+    """The host cores this process can use: the CPUs it may run on (its affinity set), bounded by
+    the cgroup's CPU quota when one is set; ``os.cpu_count()`` (every CPU of the machine) is
+    reported beside them. A CPU baseline runs one torch thread per usable core."""
+    cpu_count = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = cpu_count
+    quota = None
+    try:
+        text = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if text and text[0] != "max":
+            quota = max(1, int(int(text[0]) / int(text[1])))
+    except (OSError, ValueError, IndexError):
+        pass
+    usable = min(affinity, quota) if quota else affinity
+    return {"usable": usable, "affinity": affinity, "cgroup_quota": quota, "os_cpu_count": cpu_count}
+
+
+def _time_median(fn, budget_s: float, reps: int = 5) -> tuple[float, int]:
+    fn()  # warm
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < reps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
 def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
     """The reference's host dequant (torch CPU ops) on a bounded sample; bit-checked against dst."""
     import torch
 
     from oracle.torch_ref import host_dequant_into
 
-    threads = min(os.cpu_count() or 1, 16)
+    cores = host_cores()
+    threads = cores["usable"]
     torch.set_num_threads(threads)
     sample = regions[:10]  # 2 x each shape; ~1/11 of the pass's bytes
     elems = sum(g.numel for g in sample)
@@ -174,14 +206,7 @@ def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
         offs.append(pos)
         pos += g.numel * 2
     work = [(o, q, s, z, g.rows, g.cols) for o, q, s, z, g in zip(offs, host_q, host_s, zeros, sample)]
-    host_dequant_into(slab, work)  # warm
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        host_dequant_into(slab, work)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
+    med, runs = _time_median(lambda: host_dequant_into(slab, work), budget_s)
     # parity gate: the device output equals the reference's host computation bit for bit
     dev_bytes = torch.cat([dst[g.elem_off:g.elem_off + g.numel].view(torch.uint8).cpu() for g in sample])
     bit_exact = bool(torch.equal(dev_bytes, slab))
@@ -192,9 +217,44 @@ def cpu_baseline(regions, src, scales, dst, budget_s: float) -> dict:
         "kind": "port",
         "sample": (f"tensors 0-9 of the config-2 slab ({elems} int8 elements, {rows} rows, "
                    f"{algo} algorithmic bytes), torch CPU ops of scheduler.py:290-300 into a pinned slab, "
-                   f"median of {len(times)} runs"),
+                   f"median of {runs} runs, {threads} torch threads"),
         "ms_per_sample": round(med * 1e3, 2),
         "bit_exact_vs_device": bit_exact,
+        "host_cores": cores,
+    }
+
+
+def cpu_cast_baseline(regions, csrc, dst, budget_s: float) -> dict:
+    """The reference's host fp32→bf16 pack (``region.copy_(param.to(bf16))``, scheduler.py:1066-1071
+    and 168-181) on a bounded sample of the config-2 cast variant; bit-checked against dst."""
+    import torch
+
+    from oracle.torch_ref import host_cast_into
+
+    cores = host_cores()
+    threads = cores["usable"]
+    torch.set_num_threads(threads)
+    sample = regions[:10]
+    elems = sum(g.numel for g in sample)
+    algo = elems * 6
+    params = [csrc[g.elem_off:g.elem_off + g.numel].view(g.rows, g.cols).cpu() for g in sample]
+    slab = torch.empty(elems * 2, dtype=torch.uint8, pin_memory=True)
+    work, pos = [], 0
+    for g, p in zip(sample, params):
+        work.append((pos, p))
+        pos += g.numel * 2
+    med, runs = _time_median(lambda: host_cast_into(slab, work), budget_s)
+    dev_bytes = torch.cat([dst[g.elem_off:g.elem_off + g.numel].view(torch.uint8).cpu() for g in sample])
+    return {
+        "value": round(algo / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"tensors 0-9 of the config-2 fp32 slab ({elems} elements, {algo} algorithmic bytes), "
+                   f"torch CPU ops of scheduler.py:1066-1071 into a pinned slab, median of {runs} runs, "
+                   f"{threads} torch threads"),
+        "ms_per_sample": round(med * 1e3, 2),
+        "bit_exact_vs_device": bool(torch.equal(dev_bytes, slab)),
     }
 
 
@@ -209,7 +269,7 @@ def cpu_reference_config4_step(seed: int) -> dict:
     from oracle.torch_ref import host_dequant_into
     from bench_workloads import FluxStyleDiT, dit_linear_layers
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_cores()["usable"]
     torch.set_num_threads(threads)
     with torch.device("meta"):
         model = FluxStyleDiT(depth_double=1, depth_single=1)
@@ -265,7 +325,7 @@ def cpu_reference_config3_step(src: Path) -> dict:
 
     from stagehand_amd.registry import parse_safetensors_index
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_cores()["usable"]
     torch.set_num_threads(threads)
     out: dict = {"cores": threads, "kind": "reference ops (torch)"}
     for kind in ("double_blocks", "single_blocks"):
@@ -451,11 +511,13 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     b0 = rt.engine.bytes_h2d
+    trace_marker(args)
     t1 = time.perf_counter()
     for i in range(args.dit_steps):
         out = step(args.dit_warmup + i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t1
+    trace_marker(args)
     sent = rt.engine.bytes_h2d - b0
     ms = wall / args.dit_steps * 1e3
     hist = rt.telemetry.history[-args.dit_steps:]
@@ -508,6 +570,88 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     gc.collect()
     torch.cuda.empty_cache()
     return res
+
+
+def trace_marker(args) -> None:
+    """With ``--trace-markers``: one allocation-free unpack of 16 zero bytes, whose
+    ``sh_put_descs_kernel`` launch runs nowhere else in a streamed step. Placed before and after the
+    timed steps, the two launches bound them in a rocprofv3 kernel trace (``--trace-summary``)."""
+    if not getattr(args, "trace_markers", False):
+        return
+    import torch
+
+    from stagehand_amd.unpack import KIND_ZERO_BYTES, make_descs, unpack_noalloc
+
+    buf = torch.empty(16, dtype=torch.uint8, device="cuda")
+    unpack_noalloc(make_descs([(KIND_ZERO_BYTES, 0, 0, 1, 16, 0, 0)]), None, buf)
+    torch.cuda.synchronize()
+
+
+def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | None) -> dict:
+    """Copy/compute overlap of the marked steps in rocprofv3 CSVs (``--kernel-trace
+    --memory-copy-trace --output-format csv``): the window runs from the end of the first
+    ``sh_put_descs_kernel`` dispatch to the start of the last. Within it: the union of
+    host-to-device copy intervals, of the unpack kernels (``sh_*``) and of all other kernels
+    (the model's compute), their intersection, and, given the window's H2D bytes (the bench's
+    ``pcie_bytes_per_step`` times its steps), the H2D rate while copying."""
+    import csv
+
+    def rows(pattern: str) -> list[dict]:
+        files = sorted(trace_dir.rglob(pattern))
+        if not files:
+            raise FileNotFoundError(f"no {pattern} under {trace_dir}")
+        with open(files[0], newline="") as fh:
+            return list(csv.DictReader(fh))
+
+    kernels = rows("*kernel_trace.csv")
+    copies = rows("*memory_copy_trace.csv")
+    marks = sorted((int(k["Start_Timestamp"]), int(k["End_Timestamp"])) for k in kernels
+                   if k["Kernel_Name"].startswith("sh_put_descs_kernel"))
+    if len(marks) < 2:
+        raise ValueError("the trace has fewer than two marker dispatches (run the bench with --trace-markers)")
+    w0, w1 = marks[0][1], marks[-1][0]
+
+    def clip(iv):
+        return [(max(a, w0), min(b, w1)) for a, b in iv if b > w0 and a < w1]
+
+    marker_names = ("sh_put_descs_kernel", "sh_fill_tile_map_kernel")
+    unpack, compute = [], []
+    for k in kernels:
+        name = k["Kernel_Name"]
+        if name.startswith(marker_names):
+            continue
+        iv = (int(k["Start_Timestamp"]), int(k["End_Timestamp"]))
+        (unpack if name.startswith("sh_") else compute).append(iv)
+    h2d = [(int(c["Start_Timestamp"]), int(c["End_Timestamp"])) for c in copies
+           if c["Direction"].endswith("HOST_TO_DEVICE")]
+    d2h = [(int(c["Start_Timestamp"]), int(c["End_Timestamp"])) for c in copies
+           if c["Direction"].endswith("DEVICE_TO_HOST")]
+    h2d_w, d2h_w, comp_w, unp_w = (_union(clip(x)) for x in (h2d, d2h, compute, unpack))
+    ms = 1e-6
+    window_ms = (w1 - w0) * ms
+    h2d_busy = _length(h2d_w) * ms
+    comp_busy = _length(comp_w) * ms
+    overlap = _intersect(h2d_w, comp_w) * ms
+    out = {
+        "window_ms": round(window_ms, 2),
+        "h2d_copies": sum(1 for a, b in h2d if b > w0 and a < w1),
+        "h2d_busy_ms": round(h2d_busy, 2),
+        "h2d_busy_frac": round(h2d_busy / window_ms, 4) if window_ms else None,
+        "d2h_busy_ms": round(_length(d2h_w) * ms, 2),
+        "compute_kernels": sum(1 for a, b in compute if b > w0 and a < w1),
+        "compute_busy_ms": round(comp_busy, 2),
+        "unpack_kernels": sum(1 for a, b in unpack if b > w0 and a < w1),
+        "unpack_busy_ms": round(_length(unp_w) * ms, 2),
+        "h2d_compute_overlap_ms": round(overlap, 2),
+        "compute_hidden_frac": round(overlap / comp_busy, 4) if comp_busy else None,
+    }
+    if h2d_bytes:
+        out["h2d_bytes"] = int(h2d_bytes)
+        out["h2d_gbps_while_copying"] = round(h2d_bytes / (h2d_busy * 1e-3) / 1e9, 2) if h2d_busy else None
+        out["h2d_gbps_over_window"] = round(h2d_bytes / (window_ms * 1e-3) / 1e9, 2)
+        if pcie_gbps and out["h2d_gbps_while_copying"]:
+            out["frac_of_measured_pinned_pcie_while_copying"] = round(out["h2d_gbps_while_copying"] / pcie_gbps, 4)
+    return out
 
 
 def _dit_host_bf16(seed: int):
@@ -1053,10 +1197,19 @@ def main() -> int:
                     help="config-3 shards through every file reader, cold and warm page cache")
     ap.add_argument("--squareq-v2", default="on", choices=["on", "off"],
                     help="config 4 also from a SquareQ V2 slab (safetensors + manifest) through the file reader")
+    ap.add_argument("--trace-markers", action="store_true",
+                    help="bound the DiT legs' timed steps with marker kernels for a rocprofv3 trace")
+    ap.add_argument("--trace-summary", default=None, metavar="DIR",
+                    help="only summarise the copy/compute overlap of a rocprofv3 CSV trace in DIR (no GPU)")
+    ap.add_argument("--trace-bytes", type=int, default=None, help="H2D bytes inside the marked window")
+    ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     args = ap.parse_args()
 
+    if args.trace_summary:
+        print(json.dumps(trace_summary(Path(args.trace_summary), args.trace_bytes, args.pcie_gbps)), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the streaming path runs per GPU and this build "
               "has no multi-GPU mode (run with --gpus 1)", file=sys.stderr)
@@ -1167,6 +1320,9 @@ def main() -> int:
             "hbm_frac": round(c_gbps / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic("sh_cast_f32_bf16_kernel"),
         }
+        if not args.skip_cpu:
+            log("cpu baseline: the reference's host fp32->bf16 pack")
+            result["cast"]["cpu_baseline"] = cpu_cast_baseline(regions, csrc, dst, args.cpu_budget_s)
         del csrc
         torch.cuda.empty_cache()
         log("d2d copy and pinned H2D")
@@ -1214,8 +1370,64 @@ def main() -> int:
         log("train: config 5 streamed training step")
         result["train"] = train_leg(args)
 
+    log(summary_line(result))
     print(json.dumps(result), flush=True)
     return 0
+
+
+def summary_line(r: dict) -> str:
+    """One compact line with every leg's headline figures (the driver keeps only the end of the
+    output, and of the JSON line only the contract keys)."""
+    def g(d, *keys, default=None):
+        for k in keys:
+            if not isinstance(d, dict) or k not in d:
+                return default
+            d = d[k]
+        return d
+
+    parts = [f"dequant {r['value']:.0f} GB/s = {r['roofline']['frac']:.3f} of HBM ({r['roofline']['kernel_ms_avg']:.4f} ms)"]
+    cb = r.get("cpu_baseline")
+    if cb:
+        parts.append(f"cpu dequant {cb['value']} GB/s on {cb['cores']} cores, bit-exact {cb['bit_exact_vs_device']}")
+    c = r.get("cast")
+    if c:
+        parts.append(f"cast {c['gbps']:.0f} GB/s = {c['hbm_frac']:.3f} of HBM ({c['kernel_ms_avg']:.4f} ms)")
+        ccb = c.get("cpu_baseline")
+        if ccb:
+            parts.append(f"cpu cast {ccb['value']} GB/s, bit-exact {ccb['bit_exact_vs_device']}")
+    pcie = g(r, "pcie", "h2d_pinned_gbps")
+    if pcie:
+        parts.append(f"pinned H2D {pcie} GB/s")
+    for key, label in (("dit_squareq", "config4"), ("dit_file", "config3")):
+        d = r.get(key)
+        if not d:
+            continue
+        modes = [d[m] for m in ("staged", "pinned") if isinstance(d.get(m), dict)]
+        best = next((m for m in modes if m.get("source_mode") == d.get("best_mode")), d)
+        tl = best.get("timeline") or {}
+        parts.append(f"{label} {d['ms_per_step']} ms/step, {d['pcie_bytes_per_step'] / 1e9:.2f} GB PCIe/step, "
+                     f"{d['streamed_gbps']} GB/s = {d['streamed_gbps'] / pcie:.3f} of pinned" if pcie else
+                     f"{label} {d['ms_per_step']} ms/step")
+        if tl:
+            parts[-1] += (f", copying {tl.get('h2d_gbps_while_copying')} GB/s, "
+                          f"compute hidden {tl.get('compute_hidden_frac')}")
+        ref = d.get("reference_host_dequant_path")
+        if ref:
+            parts.append(f"{label} reference host path {ref['ms_per_step']} ms/step on {ref['cores']} cores")
+    vmm = g(r, "dit_file", "vmm")
+    if isinstance(vmm, dict) and "ms_per_step" in vmm:
+        parts.append(f"vmm {vmm['ms_per_step']} ms/step")
+    t = r.get("turbo")
+    if t:
+        for mode in ("engine_layout", "reference_layout"):
+            if isinstance(t.get(mode), dict):
+                parts.append(f"turbo/{mode} {t[mode]['ms_per_step']} ms/step, pcie {t[mode].get('pcie_frac')}")
+    tr = r.get("train")
+    if tr:
+        for mode, d in tr.items():
+            if isinstance(d, dict) and "ms_per_step" in d:
+                parts.append(f"train/{mode} {d['ms_per_step']} ms/step")
+    return "summary: " + " | ".join(parts)
 
 
 if __name__ == "__main__":
