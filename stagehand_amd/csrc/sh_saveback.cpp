@@ -13,16 +13,21 @@
 //
 // Ordering: an HSA copy cannot wait for a HIP event on the device, so each
 // submit records an event on the caller's stream and a worker thread waits
-// for it on the host before it issues the copies. Completion is an HSA signal
-// (initialised to the number of copies; each finished copy decrements it).
-// Tickets complete in submission order: query and wait report a ticket done
-// only when every live earlier ticket is, so a later ticket covers earlier
-// copies as a later event on one stream would.
+// for it on the host before it issues the copies. Completion: each copy has an
+// HSA signal of its own, initialised to 1, which the copy engine decrements. (HSA
+// lets several copies share one signal initialised to their count, but the
+// profiler's copy tracing replaces each copy's completion signal and forwards
+// one completion per copy: with a shared signal it reported "bad original signal
+// value" and completions that were never delivered.) Tickets complete in
+// submission order: query and wait report a ticket done only when every live
+// earlier ticket is, so a later ticket covers earlier copies as a later event on
+// one stream would.
 
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
 
+#include <algorithm>
 #include <atomic>
 #include <condition_variable>
 #include <cstdint>
@@ -38,7 +43,7 @@
 
 namespace {
 
-// A ticket's state. Its signal and fence belong to the object and are destroyed with it,
+// A ticket's state. Its signals and fence belong to the object and are destroyed with it,
 // when the last reference drops: the queue's, the worker's, a waiter's snapshot or the
 // engine's map entry. Releasing a ticket therefore never frees a signal that a waiter on a
 // later ticket, or the worker, still holds.
@@ -46,16 +51,16 @@ struct Job {
   uint64_t id = 0;
   hipEvent_t fence = nullptr;  // none for a ticket without copies
   std::vector<sh_copy_item> items;
-  hsa_signal_t done{0};
-  int status = SH_OK;  // set (under the engine lock) before a failure completes `done`
+  std::vector<hsa_signal_t> done;  // done[k]: 1 until items[k] has been copied
+  int status = SH_OK;  // set (under the engine lock) before a failure completes the signals
   std::string error;
-  uint64_t issue_ticks = 0;  // HSA system clock when the worker issued the first copy (timing only)
 
   Job() = default;
   Job(const Job&) = delete;
   Job& operator=(const Job&) = delete;
   ~Job() {
-    if (done.handle != 0) hsa_signal_destroy(done);
+    for (hsa_signal_t s : done)
+      if (s.handle != 0) hsa_signal_destroy(s);
     if (fence != nullptr) (void)hipEventDestroy(fence);
   }
 };
@@ -87,14 +92,15 @@ struct sh_saveback {
 
 namespace {
 
-// Records a failure, then completes the job's signal (waiters read the status after the signal).
-void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, hsa_signal_value_t outstanding) {
+// Records a failure, then completes the signals of the copies from `first` on, which were
+// never issued (waiters read the status after the signals).
+void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, size_t first) {
   {
     std::lock_guard<std::mutex> lk(sb->mu);
     j.status = status;
     j.error = what;
   }
-  hsa_signal_subtract_screlease(j.done, outstanding);
+  for (size_t k = first; k < j.done.size(); ++k) hsa_signal_subtract_screlease(j.done[k], 1);
 }
 
 void worker_loop(sh_saveback* sb) {
@@ -109,37 +115,44 @@ void worker_loop(sh_saveback* sb) {
       j = sb->queue.front();
       sb->queue.pop_front();
     }
-    const hsa_signal_value_t n = (hsa_signal_value_t)j->items.size();
     hipError_t e = hipEventSynchronize(j->fence);
     if (e != hipSuccess) {
-      fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), n);
+      fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), 0);
       continue;
     }
-    if (sb->timing.load()) hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &j->issue_ticks);
-    hsa_signal_value_t issued = 0;
-    for (const sh_copy_item& it : j->items) {
-      hsa_status_t s = hsa_amd_memory_async_copy(it.dst, sb->cpu, it.src, sb->gpu, it.bytes, 0, nullptr, j->done);
+    for (size_t k = 0; k < j->items.size(); ++k) {
+      const sh_copy_item& it = j->items[k];
+      hsa_status_t s = hsa_amd_memory_async_copy(it.dst, sb->cpu, it.src, sb->gpu, it.bytes, 0, nullptr, j->done[k]);
       if (s != HSA_STATUS_SUCCESS) {
         const char* msg = nullptr;
         hsa_status_string(s, &msg);
-        // the copies already issued still decrement the signal themselves
-        fail_job(sb, *j, SH_ERR_HIP, std::string("hsa_amd_memory_async_copy: ") + (msg ? msg : "error"), n - issued);
+        // the copies already issued complete their own signals
+        fail_job(sb, *j, SH_ERR_HIP, std::string("hsa_amd_memory_async_copy: ") + (msg ? msg : "error"), k);
         break;
       }
-      ++issued;
     }
   }
 }
 
 // Waits for `j` alone; SH_OK or its failure (recorded in the last error).
 int wait_job(sh_saveback* sb, const std::shared_ptr<Job>& j) {
-  hsa_signal_value_t v;
-  while ((v = hsa_signal_wait_scacquire(j->done, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, HSA_WAIT_STATE_BLOCKED)) >= 1) {
+  bool negative = false;
+  for (hsa_signal_t s : j->done) {
+    hsa_signal_value_t v;
+    while ((v = hsa_signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, HSA_WAIT_STATE_BLOCKED)) >= 1) {
+    }
+    negative = negative || v < 0;
   }
   std::lock_guard<std::mutex> lk(sb->mu);
   if (j->status != SH_OK) return sh::fail(j->status, "save-back ticket %llu: %s", (unsigned long long)j->id, j->error.c_str());
-  if (v < 0) return sh::fail(SH_ERR_HIP, "save-back ticket %llu: the copy engine reported an error", (unsigned long long)j->id);
+  if (negative) return sh::fail(SH_ERR_HIP, "save-back ticket %llu: the copy engine reported an error", (unsigned long long)j->id);
   return SH_OK;
+}
+
+bool job_done(const Job& j) {
+  for (hsa_signal_t s : j.done)
+    if (hsa_signal_load_scacquire(s) >= 1) return false;
+  return true;
 }
 
 // The live jobs up to and including `ticket` (in order); SH_ERR_INVALID for a ticket never issued.
@@ -224,12 +237,15 @@ extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, ui
       return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: item %llu has a NULL pointer", (unsigned long long)i);
     j->items.push_back(items[i]);
   }
-  if (hsa_signal_create((hsa_signal_value_t)j->items.size(), 0, nullptr, &j->done) != HSA_STATUS_SUCCESS) {
-    j->done.handle = 0;
-    return sh::fail(SH_ERR_HIP, "sh_saveback_submit: hsa_signal_create failed");
+  j->done.reserve(j->items.size());
+  for (size_t k = 0; k < j->items.size(); ++k) {
+    hsa_signal_t s{0};
+    if (hsa_signal_create(1, 0, nullptr, &s) != HSA_STATUS_SUCCESS)
+      return sh::fail(SH_ERR_HIP, "sh_saveback_submit: hsa_signal_create failed");
+    j->done.push_back(s);
   }
-  // A ticket without copies is complete at once (its signal starts at 0): it gets no fence
-  // and never reaches the worker, which only waits for fences and issues copies.
+  // A ticket without copies is complete at once (it has no signals): it gets no fence and
+  // never reaches the worker, which only waits for fences and issues copies.
   const bool empty = j->items.empty();
   if (!empty) {
     hipError_t e = hipEventCreateWithFlags(&j->fence, hipEventDisableTiming);
@@ -255,8 +271,8 @@ extern "C" int sh_saveback_query(sh_saveback* sb, uint64_t ticket) {
   int st = jobs_upto(sb, ticket, js, "sh_saveback_query");
   if (st != SH_OK) return st;
   for (const auto& j : js) {
-    if (hsa_signal_load_scacquire(j->done) >= 1) return SH_ERR_NOT_READY;
-    st = wait_job(sb, j);  // already at its final value: returns at once
+    if (!job_done(*j)) return SH_ERR_NOT_READY;
+    st = wait_job(sb, j);  // every signal at its final value: returns at once
     if (st != SH_OK) return st;
   }
   return SH_OK;
@@ -342,13 +358,17 @@ extern "C" int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64
   if (st != SH_OK) return st;
   out2[0] = out2[1] = 0;
   if (j->items.empty()) return SH_OK;
-  hsa_amd_profiling_async_copy_time_t t{};
-  if (hsa_amd_profiling_get_async_copy_time(j->done, &t) != HSA_STATUS_SUCCESS || t.end == 0)
-    return sh::fail(SH_ERR_STATE, "sh_saveback_ticket_times: the ticket was submitted without timing");
-  // the signal holds the last copy's times; a ticket of several copies starts no later than its first issue
-  uint64_t start = t.start;
-  if (j->items.size() > 1 && j->issue_ticks != 0 && j->issue_ticks < start) start = j->issue_ticks;
+  // each copy's signal holds that copy's engine start and end times
+  uint64_t start = UINT64_MAX, end = 0;
+  for (hsa_signal_t s : j->done) {
+    hsa_amd_profiling_async_copy_time_t t{};
+    if (hsa_amd_profiling_get_async_copy_time(s, &t) != HSA_STATUS_SUCCESS || t.end == 0)
+      return sh::fail(SH_ERR_STATE, "sh_saveback_ticket_times: no copy times (the ticket was submitted without "
+                                    "timing, or a tool replaced its copies' completion signals)");
+    start = std::min<uint64_t>(start, t.start);
+    end = std::max<uint64_t>(end, t.end);
+  }
   out2[0] = ticks_to_ns(start);
-  out2[1] = ticks_to_ns(t.end);
+  out2[1] = ticks_to_ns(end);
   return SH_OK;
 }

@@ -551,14 +551,18 @@ class AsyncTransferEngine:
         torch.cuda.synchronize()
         ref = self._trace_ref
         compute = [(bid, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev)) for bid, s_ev, e_ev in self._trace_compute]
-        d2h = []
+        d2h, untimed = [], 0
         for n, s_ev, e_ev, kind in self._trace_d2h:
             if isinstance(s_ev, SaveBackTicket):  # copy-engine times, aligned at start_trace
-                t0, t1 = s_ev.times_ns()
+                try:
+                    t0, t1 = s_ev.times_ns()
+                except RuntimeError:  # a tool (a profiler's copy tracing) took the copies' signals
+                    untimed += 1
+                    continue
                 d2h.append((n, (t0 - self._trace_t0_ns) / 1e6, (t1 - self._trace_t0_ns) / 1e6, kind))
             else:
                 d2h.append((n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind))
-        out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h}
+        out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h, "d2h_untimed": untimed}
         _native.call("sh_loader_set_timing", self._loader_handle(), 0)
         if self._saveback is not None:
             self._saveback.set_timing(False)
