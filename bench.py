@@ -654,6 +654,27 @@ def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | Non
     return out
 
 
+def pmc_summary(dirs: list[Path]) -> dict:
+    """Per-kernel medians of every counter in rocprofv3 ``--pmc`` CSVs (``*counter_collection.csv``
+    under each directory), for the library's kernels (names starting with ``sh_``), with the
+    kernels' median dispatch durations in ns."""
+    import csv
+    import statistics
+
+    vals: dict[str, dict[str, list[float]]] = {}
+    for d in dirs:
+        for f in sorted(Path(d).rglob("*counter_collection.csv")):
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    name = row["Kernel_Name"]
+                    if not name.startswith("sh_"):
+                        continue
+                    k = vals.setdefault(name, {})
+                    k.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+                    k.setdefault("_duration_ns", []).append(float(row["End_Timestamp"]) - float(row["Start_Timestamp"]))
+    return {name: {c: statistics.median(v) for c, v in sorted(cs.items())} for name, cs in sorted(vals.items())}
+
+
 def _dit_host_bf16(seed: int):
     """The 12B DiT with every block parameter in host memory as bf16: N(0, 0.02)
     drawn on the device (fast), RMSNorm weights ones; frozen."""
@@ -1202,6 +1223,8 @@ def main() -> int:
     ap.add_argument("--trace-summary", default=None, metavar="DIR",
                     help="only summarise the copy/compute overlap of a rocprofv3 CSV trace in DIR (no GPU)")
     ap.add_argument("--trace-bytes", type=int, default=None, help="H2D bytes inside the marked window")
+    ap.add_argument("--pmc-summary", nargs="+", default=None, metavar="DIR",
+                    help="only print per-kernel medians of rocprofv3 --pmc CSVs under DIRs (no GPU)")
     ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
@@ -1209,6 +1232,9 @@ def main() -> int:
 
     if args.trace_summary:
         print(json.dumps(trace_summary(Path(args.trace_summary), args.trace_bytes, args.pcie_gbps)), flush=True)
+        return 0
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary([Path(d) for d in args.pmc_summary]), indent=1), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the streaming path runs per GPU and this build "
