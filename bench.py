@@ -402,6 +402,8 @@ def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
                                         vram_low_watermark_mb=14400, prefetch_window_blocks=2,
                                         max_inflight_transfers=3, nan_inf_check=False, strict_bf16=False,
                                         telemetry_enabled=True, pinned_source_cache=pinned, file_reader=reader)
+    if getattr(args, "run_ahead", None) is not None:
+        cfg.max_run_ahead_blocks = args.run_ahead
     cfg.telemetry_file = None
     return cfg
 
@@ -444,6 +446,30 @@ def _intersect(x: list[tuple[float, float]], y: list[tuple[float, float]]) -> fl
         else:
             j += 1
     return tot
+
+
+def load_gap_causes(trace: dict, top: int = 6) -> list[dict]:
+    """For the longest gaps between consecutive block loads of a traced step (one copy's end to the
+    next copy's start): when the next load was submitted by the host relative to the gap, and the
+    host waits (``AsyncTransferEngine.host_wait``) that overlapped the gap before that submit."""
+    loads = sorted(trace["loads"], key=lambda l: l[2])
+    waits = trace.get("host_waits") or []
+    gaps = []
+    for a, b in zip(loads, loads[1:]):
+        g0, g1 = a[3], b[2]
+        if g1 - g0 <= 1.0:
+            continue
+        submit = b[5] if len(b) > 5 else None
+        until = min(g1, submit) if submit is not None else g1
+        by_kind: dict[str, float] = {}
+        for kind, w0, w1 in waits:
+            ov = min(w1, until) - max(w0, g0)
+            if ov > 0:
+                by_kind[kind] = round(by_kind.get(kind, 0.0) + ov, 2)
+        gaps.append({"gap_ms": round(g1 - g0, 2), "at_ms": round(g0, 1), "next_block": b[0],
+                     "submitted_ms_after_gap_start": None if submit is None else round(submit - g0, 2),
+                     "host_waits_before_submit_ms": by_kind})
+    return sorted(gaps, key=lambda g: -g["gap_ms"])[:top]
 
 
 def timeline_stats(trace: dict, pcie_peak_gbps: float | None) -> dict:
@@ -797,7 +823,8 @@ def train_leg(args) -> dict:
         cfg = stagehand.StagehandConfig(pinned_pool_mb=4096, pinned_slab_mb=256, vram_high_watermark_mb=19200,
                                         vram_low_watermark_mb=14400, prefetch_window_blocks=3, max_inflight_transfers=4,
                                         nan_inf_check=False, strict_bf16=False, telemetry_enabled=True,
-                                        frozen_host_copies=fhc, save_back_engine=args.save_back)
+                                        frozen_host_copies=fhc, save_back_engine=args.save_back,
+                                        **({} if args.run_ahead is None else {"max_run_ahead_blocks": args.run_ahead}))
         cfg.telemetry_file = None
         rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
                                         inference_mode=False)
@@ -822,11 +849,13 @@ def train_leg(args) -> dict:
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
         h0, d0 = rt.engine.bytes_h2d, rt.engine.bytes_d2h
+        rt.engine.host_wait_ms.clear()
         t1 = time.perf_counter()
         for i in range(args.train_steps):
             step(args.train_warmup + i)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t1
+        host_waits = {k: round(v / args.train_steps, 1) for k, v in sorted(rt.engine.host_wait_ms.items())}
         ms = wall / args.train_steps * 1e3
         h2d = (rt.engine.bytes_h2d - h0) // args.train_steps
         d2h = (rt.engine.bytes_d2h - d0) // args.train_steps
@@ -842,7 +871,9 @@ def train_leg(args) -> dict:
                                                        sorted(trace["loads"], key=lambda l: l[2])[1:])),
                 reverse=True)[:8]
             timeline["first_load_ms"] = round(t_first, 2)
+            timeline["load_gap_causes"] = load_gap_causes(trace)
         res = {"ms_per_step": round(ms, 1), "h2d_bytes_per_step": h2d, "d2h_bytes_per_step": d2h, "timeline": timeline,
+               "host_wait_ms_per_step": host_waits,
                "h2d_gbps": round(h2d / (ms * 1e-3) / 1e9, 2), "d2h_gbps": round(d2h / (ms * 1e-3) / 1e9, 2),
                "block_bytes": sum(e.size_bytes for e in rt.registry.blocks_in_order()),
                "peak_vram_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
@@ -1226,6 +1257,8 @@ def main() -> int:
     ap.add_argument("--pmc-summary", nargs="+", default=None, metavar="DIR",
                     help="only print per-kernel medians of rocprofv3 --pmc CSVs under DIRs (no GPU)")
     ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
+    ap.add_argument("--run-ahead", type=int, default=None,
+                    help="config 5: StagehandConfig.max_run_ahead_blocks (default: the config's)")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     args = ap.parse_args()

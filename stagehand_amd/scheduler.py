@@ -24,6 +24,7 @@ and casts into CPU tensors); SquareQ dequantisation exists only on the device.
 from __future__ import annotations
 
 import collections
+import contextlib
 
 import logging
 import mmap
@@ -267,7 +268,13 @@ class StagehandScheduler:
         for bid in ids:
             ev = self._d2h_fences.pop(bid)
             if ev is not None:
-                ev.synchronize()
+                with self._host_wait("d2h_fence"):
+                    ev.synchronize()
+
+    def _host_wait(self, kind: str):
+        """The engine's host-wait accounting (a no-op context for engines without it)."""
+        wait = getattr(self._engine, "host_wait", None)
+        return wait(kind) if wait is not None else contextlib.nullcontext()
 
     def _save_params_to_host(self, block_id: str, module: nn.Module, names: list[str], with_grads: bool = False) -> None:
         """``param.data = param.data.to("cpu").clone()`` for ``names`` (and grads), without a host sync.
@@ -460,7 +467,9 @@ class StagehandScheduler:
         """Host wait for the compute of the block ``max_run_ahead_blocks`` back."""
         limit = getattr(self._config, "max_run_ahead_blocks", 0)
         while limit > 0 and len(self._done_marks) >= limit:
-            self._done_marks.popleft().synchronize()
+            mark = self._done_marks.popleft()
+            with self._host_wait("run_ahead"):
+                mark.synchronize()
 
     def _mark_block_done(self) -> None:
         if self._has_cuda and getattr(self._config, "max_run_ahead_blocks", 0) > 0:

@@ -26,6 +26,8 @@ import logging
 import os
 import threading
 import time
+from collections import Counter
+from contextlib import contextmanager
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any
 
@@ -190,6 +192,7 @@ class TransferHandle:
     ticket: int | None = None
     keepalive: list = field(default_factory=list, repr=False)
     device_waited: bool = False
+    host_clock: bool = False  # submitted_at is on time.perf_counter (set while a trace runs)
 
 
 @dataclass
@@ -258,6 +261,10 @@ class AsyncTransferEngine:
         self._save_back = save_back
         self._saveback: SaveBackEngine | None = None
         self._trace_t0_ns = 0
+        self._trace_t0_host = 0.0
+        self._trace_waits: list[tuple[str, float, float]] = []
+        # host time spent waiting, by kind (ms): see host_wait
+        self.host_wait_ms: Counter = Counter()
         # optional device timeline (start_trace / stop_trace)
         self._trace_ref: NativeEvent | None = None
         self._trace_loads: list[tuple[str, int, float, float, float]] = []
@@ -466,6 +473,8 @@ class AsyncTransferEngine:
             self._raise_transfer(st, block_id, "load")
         handle.ticket = ticket.value
         handle.keepalive = keep
+        if self._trace_ref is not None:
+            handle.submitted_at, handle.host_clock = time.perf_counter(), True
         self.bytes_h2d += source.src_bytes
         self.loads += 1
         with self._lock:
@@ -516,17 +525,33 @@ class AsyncTransferEngine:
             sb.set_timing(True)
         self._trace_ref = NativeEvent(timing=True)
         self._trace_ref.record(_current_stream_handle())
+        # host times are aligned with the device timeline when the reference event completes
+        self._trace_ref.synchronize()
+        self._trace_t0_host = time.perf_counter()
         if sb is not None:
-            # copy-engine times are read on the HSA system clock: take its value when the reference completes
-            self._trace_ref.synchronize()
+            # copy-engine times are read on the HSA system clock: take its value then too
             self._trace_t0_ns = sb.clock_ns()
         self._trace_loads = []
         self._trace_compute = []
         self._trace_d2h = []
+        self._trace_waits = []
 
     @property
     def tracing(self) -> bool:
         return self._trace_ref is not None
+
+    @contextmanager
+    def host_wait(self, kind: str):
+        """Accounts the host time spent in the block under ``kind`` (``host_wait_ms``); while a trace
+        runs, also records the interval on the trace's timeline (ms after ``start_trace``)."""
+        t0 = time.perf_counter()
+        try:
+            yield
+        finally:
+            t1 = time.perf_counter()
+            self.host_wait_ms[kind] += (t1 - t0) * 1e3
+            if self._trace_ref is not None:
+                self._trace_waits.append((kind, (t0 - self._trace_t0_host) * 1e3, (t1 - self._trace_t0_host) * 1e3))
 
     def mark_compute(self, block_id: str, start: bool) -> None:
         if self._trace_ref is None:
@@ -562,12 +587,13 @@ class AsyncTransferEngine:
                 d2h.append((n, (t0 - self._trace_t0_ns) / 1e6, (t1 - self._trace_t0_ns) / 1e6, kind))
             else:
                 d2h.append((n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind))
-        out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h, "d2h_untimed": untimed}
+        out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h, "d2h_untimed": untimed,
+               "host_waits": list(self._trace_waits)}
         _native.call("sh_loader_set_timing", self._loader_handle(), 0)
         if self._saveback is not None:
             self._saveback.set_timing(False)
         self._trace_ref = None
-        self._trace_loads, self._trace_compute, self._trace_d2h = [], [], []
+        self._trace_loads, self._trace_compute, self._trace_d2h, self._trace_waits = [], [], [], []
         return out
 
     def _record_ticket_times(self, handle: TransferHandle) -> None:
@@ -576,7 +602,8 @@ class AsyncTransferEngine:
         out = (ctypes.c_float * 3)()
         st = _native.lib().sh_loader_ticket_times(self._loader, handle.ticket, self._trace_ref.handle, out)
         if st == _native.SH_OK:
-            self._trace_loads.append((handle.block_id, handle.size_bytes, out[0], out[1], out[2]))
+            submit = (handle.submitted_at - self._trace_t0_host) * 1e3 if handle.host_clock else None
+            self._trace_loads.append((handle.block_id, handle.size_bytes, out[0], out[1], out[2], submit))
 
     # ── asynchronous parameter save-back ─────────────────────────────
 
@@ -699,7 +726,8 @@ class AsyncTransferEngine:
                 if not self._pending_d2h:
                     return
                 ev = self._pending_d2h[0][0]
-            ev.synchronize()
+            with self.host_wait("save_back_backlog"):
+                ev.synchronize()
             self._reap_d2h()
 
     def _reap_d2h(self, block: bool = False) -> None:
@@ -763,12 +791,13 @@ class AsyncTransferEngine:
             self._complete_handle(handle)
             return
         t0 = time.monotonic()
-        if handle.ticket is not None:
-            st = _native.lib().sh_loader_sync(self._loader, handle.ticket)
-            if st != _native.SH_OK:
-                self._raise_transfer(st, handle.block_id, handle.direction, handle)
-        else:
-            handle.event.synchronize()
+        with self.host_wait("transfer_wait"):
+            if handle.ticket is not None:
+                st = _native.lib().sh_loader_sync(self._loader, handle.ticket)
+                if st != _native.SH_OK:
+                    self._raise_transfer(st, handle.block_id, handle.direction, handle)
+            else:
+                handle.event.synchronize()
         self.wait_device(handle)
         elapsed_ms = (time.monotonic() - t0) * 1000.0
         if _STALL_LOGS_ENABLED and elapsed_ms > 1.0:
@@ -867,15 +896,16 @@ class AsyncTransferEngine:
                 if len(self._inflight) < self._max_inflight:
                     break
                 oldest = self._inflight[0]
-            if oldest.ticket is not None:
-                st = _native.lib().sh_loader_sync(self._loader, oldest.ticket)
-                if st != _native.SH_OK:
-                    self._raise_transfer(st, oldest.block_id, oldest.direction)
-            elif oldest.event is not None:
-                oldest.event.synchronize()
-            else:
-                with self._cond:
-                    self._cond.wait(timeout=0.001)
+            with self.host_wait("inflight_slot"):
+                if oldest.ticket is not None:
+                    st = _native.lib().sh_loader_sync(self._loader, oldest.ticket)
+                    if st != _native.SH_OK:
+                        self._raise_transfer(st, oldest.block_id, oldest.direction)
+                elif oldest.event is not None:
+                    oldest.event.synchronize()
+                else:
+                    with self._cond:
+                        self._cond.wait(timeout=0.001)
         waited_ms = (time.monotonic() - t0) * 1000.0
         if waited_ms > 1.0:
             log.debug("AsyncTransferEngine: backpressure wait %.2f ms", waited_ms)
