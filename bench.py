@@ -814,6 +814,12 @@ def train_leg(args) -> dict:
     modes = (("reference_eviction", False), ("frozen_host_copies", True))
     if args.train_modes == "reference":
         modes = modes[:1]
+    if args.release_accounting == "off":
+        # A/B of the eviction loop's release accounting: the budget counts the device memory that
+        # save-backs in flight still hold, as it would without StagehandScheduler's hookup
+        from stagehand_amd.budget import BudgetManager
+
+        BudgetManager.count_as_released = lambda self, releasing_bytes: None
     for label, fhc in modes:
         t0 = time.perf_counter()
         with torch.device("meta"):
@@ -848,7 +854,7 @@ def train_leg(args) -> dict:
             step(i)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
-        h0, d0 = rt.engine.bytes_h2d, rt.engine.bytes_d2h
+        h0, d0, l0 = rt.engine.bytes_h2d, rt.engine.bytes_d2h, rt.engine.loads
         rt.engine.host_wait_ms.clear()
         t1 = time.perf_counter()
         for i in range(args.train_steps):
@@ -856,6 +862,7 @@ def train_leg(args) -> dict:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t1
         host_waits = {k: round(v / args.train_steps, 1) for k, v in sorted(rt.engine.host_wait_ms.items())}
+        loads = rt.engine.loads - l0
         ms = wall / args.train_steps * 1e3
         h2d = (rt.engine.bytes_h2d - h0) // args.train_steps
         d2h = (rt.engine.bytes_d2h - d0) // args.train_steps
@@ -873,6 +880,7 @@ def train_leg(args) -> dict:
             timeline["first_load_ms"] = round(t_first, 2)
             timeline["load_gap_causes"] = load_gap_causes(trace)
         res = {"ms_per_step": round(ms, 1), "h2d_bytes_per_step": h2d, "d2h_bytes_per_step": d2h, "timeline": timeline,
+               "loads_per_step": round(loads / args.train_steps, 1),
                "host_wait_ms_per_step": host_waits,
                "h2d_gbps": round(h2d / (ms * 1e-3) / 1e9, 2), "d2h_gbps": round(d2h / (ms * 1e-3) / 1e9, 2),
                "block_bytes": sum(e.size_bytes for e in rt.registry.blocks_in_order()),
@@ -1257,6 +1265,8 @@ def main() -> int:
     ap.add_argument("--pmc-summary", nargs="+", default=None, metavar="DIR",
                     help="only print per-kernel medians of rocprofv3 --pmc CSVs under DIRs (no GPU)")
     ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
+    ap.add_argument("--release-accounting", default="on", choices=["on", "off"],
+                    help="config 5: off counts save-back-held memory as used (A/B of the eviction loop)")
     ap.add_argument("--run-ahead", type=int, default=None,
                     help="config 5: StagehandConfig.max_run_ahead_blocks (default: the config's)")
     ap.add_argument("--train-steps", type=int, default=3)
