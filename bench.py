@@ -900,10 +900,88 @@ def train_leg(args) -> dict:
     return out
 
 
-def _vmm_run(args, src: Path) -> dict:
+def vmm_latency_leg(args) -> dict:
+    """The VMM allocator against the reference's published latencies (README.md:165-170, RTX 3090:
+    ensure_resident hot path 250 ns median, ensure_resident + as_tensor 1.4 us median, eviction +
+    re-map of a 1.5 GB region 4.2 ms median): the fast path timed natively and from Python, and a
+    1.5 GB region mapped while the ceiling forces another one out."""
+    import statistics
+
+    import torch
+
+    from stagehand_amd.vmm import SlabAllocator
+
+    stream = torch.cuda.current_stream().cuda_stream
+    out: dict = {}
+    alloc = SlabAllocator(device=torch.cuda.current_device())
+    gran = alloc.granularity()
+    size = -(-(64 << 20) // gran) * gran
+    slab = alloc.create_slab(size)
+    reg = alloc.define_region(slab, 0, size)
+    runs = [alloc.time_fast_path(slab, reg, stream, 100_000) for _ in range(5)]
+    out["native_ensure_ns"] = round(statistics.median(r[0] for r in runs), 1)
+    out["native_ensure_release_ns"] = round(statistics.median(r[1] for r in runs), 1)
+
+    def median_us(fn, n=20_000):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter_ns()
+            fn()
+            ts.append(time.perf_counter_ns() - t0)
+        return round(statistics.median(ts) / 1e3, 3)
+
+    held = []
+    out["python_ensure_us"] = median_us(lambda: held.append(alloc.ensure_resident(slab, reg, stream)))
+    for h in held:
+        h.release()
+    held.clear()
+
+    def ensure_tensor():
+        h = alloc.ensure_resident(slab, reg, stream)
+        held.append((h, h.as_tensor("bfloat16", [size // 2])))
+
+    out["python_ensure_as_tensor_us"] = median_us(ensure_tensor)
+    for h, t in held:
+        del t
+        h.release()
+    held.clear()
+    alloc.destroy_slab(slab)
+    alloc.close()
+
+    # eviction + re-map: two 1.5 GB regions under a 2 GB ceiling; each ensure_resident of the one
+    # not mapped unmaps the other (its handle released, the stream idle) and maps it. An eviction
+    # lowers the slab's watermark to the evicted region (vmm_src/eviction.rs:130-131), so the
+    # watermark is re-opened with set_priority (vmm_backend.py activate_model) before each call
+    big = -(-(1536 << 20) // gran) * gran
+    alloc = SlabAllocator(device=torch.cuda.current_device(), ceiling_mb=2048)
+    slab = alloc.create_slab(2 * big)
+    regs = [alloc.define_region(slab, i * big, big) for i in range(2)]
+    alloc.ensure_resident(slab, regs[0], stream).release()
+    ts = []
+    for i in range(1, 21):
+        alloc.set_priority(slab, i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        h = alloc.ensure_resident(slab, regs[i % 2], stream)
+        ts.append((time.perf_counter() - t0) * 1e3)
+        h.release()
+    st = alloc.stats()
+    out["evict_remap_1p5gb_ms"] = round(statistics.median(ts), 3)
+    out["evict_remap_1p5gb_ms_min_max"] = [round(min(ts), 3), round(max(ts), 3)]
+    out["region_bytes"] = big
+    out["granularity"] = gran
+    out["reference_rtx3090"] = {"ensure_resident_ns": 250, "ensure_as_tensor_us": 1.4, "evict_remap_1p5gb_ms": 4.2}
+    alloc.destroy_slab(slab)
+    alloc.close()
+    log(f"vmm latency: {out}")
+    return out
+
+
+def _vmm_run(args, src: Path, ceiling_mb: int | None = None) -> dict:
     """Config-3 DiT served from the VMM backend: every block registered in one slab,
     filled from the sharded safetensors on first use (native loads), then resident
-    in mapped device memory under the default ceiling."""
+    in mapped device memory under the default ceiling, or under ``ceiling_mb``, which
+    evicts and refills regions every step."""
     import gc
 
     import torch
@@ -919,6 +997,8 @@ def _vmm_run(args, src: Path) -> dict:
     if handle is None:
         rt.shutdown()
         return {"skipped": "VMM backend unavailable"}
+    if ceiling_mb is not None:
+        rt.vmm.allocator.set_vram_ceiling(int(ceiling_mb) << 20)
     img, txt, vec = _dit_inputs(args.seed)
     served = {"vmm": 0, "swap": 0}
     orig = rt._vmm_before_block
@@ -946,26 +1026,40 @@ def _vmm_run(args, src: Path) -> dict:
         step(1 + i)
     torch.cuda.synchronize()
     served = {"vmm": 0, "swap": 0}
+    st0 = rt.vmm.stats()
+    h2d0 = rt.engine.bytes_h2d
     t1 = time.perf_counter()
     for i in range(args.dit_steps):
         out = step(1 + args.dit_warmup + i)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t1) / args.dit_steps * 1e3
+    st1 = rt.vmm.stats()
+    h2d = (rt.engine.bytes_h2d - h2d0) / args.dit_steps
     # fast path: ensure_resident + release of a resident region, through the Python binding
     alloc = rt.vmm.allocator
     stream = torch.cuda.current_stream().cuda_stream
     n = 2000
-    t2 = time.perf_counter()
-    for _ in range(n):
-        alloc.ensure_resident(handle.slab_id, handle.regions[0], stream).release()
-    fast_us = (time.perf_counter() - t2) / n * 1e6
+    fast_us = None
+    try:
+        t2 = time.perf_counter()
+        for _ in range(n):
+            alloc.ensure_resident(handle.slab_id, handle.regions[0], stream).release()
+        fast_us = round((time.perf_counter() - t2) / n * 1e6, 2)
+    except MemoryError:  # under a tight ceiling the region may be evicted and above the watermark
+        pass
     st = rt.vmm.stats()
     res = {"file_reader": args.file_reader, "first_step_ms": round(first_ms, 1), "ms_per_step": round(ms, 2),
            "steps": args.dit_steps,
            "blocks_served_per_step": {k: v / args.dit_steps for k, v in served.items()},
            "mapped_gb": round(st["mapped_bytes"] / 1e9, 2), "vram_ceiling_gb": round(st["vram_ceiling"] / 1e9, 1),
            "granularity": st["granularity"], "maps": st["maps"], "evictions": st["evictions"],
-           "ensure_release_fast_path_us": round(fast_us, 2), "out_finite": bool(torch.isfinite(out.float()).all())}
+           "ensure_release_fast_path_us": fast_us, "out_finite": bool(torch.isfinite(out.float()).all()),
+           "evictions_per_step": (st1["evictions"] - st0["evictions"]) / args.dit_steps,
+           "maps_per_step": (st1["maps"] - st0["maps"]) / args.dit_steps,
+           "refill_bytes_per_step": int(h2d),
+           "refill_gbps": round(h2d / (ms * 1e-3) / 1e9, 2)}
+    if getattr(args, "pcie_peak_gbps", None):
+        res["refill_frac_of_measured_pcie"] = round(res["refill_gbps"] / args.pcie_peak_gbps, 4)
     log(f"dit/vmm: {res}")
     rt.shutdown()
     del rt, model, out
@@ -1184,6 +1278,8 @@ def dit_leg(kind: str, args) -> dict:
     if kind == "file" and args.vmm == "on":
         log("dit/file: served from the VMM backend")
         res["vmm"] = _vmm_run(args, src)
+        log("dit/file: served from the VMM backend under a 19.2 GB ceiling (regions evicted and refilled)")
+        res["vmm_tight"] = _vmm_run(args, src, ceiling_mb=19200)
     shutil.rmtree(workdir, ignore_errors=True)
     return res
 
@@ -1304,6 +1400,8 @@ def main() -> int:
             out["dit_squareq"] = dit_leg("squareq", args)
         if args.dit in ("file", "both"):
             out["dit_file"] = dit_leg("file", args)
+        if args.vmm == "on":
+            out["vmm_latency"] = vmm_latency_leg(args)
         if args.turbo == "on":
             out["turbo"] = turbo_leg(args)
         if args.train == "on":
@@ -1432,6 +1530,9 @@ def main() -> int:
         log("dit: config 3 (file-backed bf16) streaming")
         result["dit_file"] = dit_leg("file", args)
         torch.cuda.empty_cache()
+    if args.vmm == "on":
+        log("vmm: allocator latencies")
+        result["vmm_latency"] = vmm_latency_leg(args)
     if args.turbo == "on":
         log("turbo: config 3 DiT through the window engine")
         result["turbo"] = turbo_leg(args)
@@ -1486,6 +1587,14 @@ def summary_line(r: dict) -> str:
     vmm = g(r, "dit_file", "vmm")
     if isinstance(vmm, dict) and "ms_per_step" in vmm:
         parts.append(f"vmm {vmm['ms_per_step']} ms/step")
+    vt = g(r, "dit_file", "vmm_tight")
+    if isinstance(vt, dict) and "ms_per_step" in vt:
+        parts.append(f"vmm 19.2 GB ceiling {vt['ms_per_step']} ms/step, {vt['evictions_per_step']} evictions/step, "
+                     f"refill {vt['refill_gbps']} GB/s")
+    vl = r.get("vmm_latency")
+    if isinstance(vl, dict) and "native_ensure_ns" in vl:
+        parts.append(f"vmm ensure {vl['native_ensure_ns']} ns native, {vl['python_ensure_us']} us python, "
+                     f"+as_tensor {vl['python_ensure_as_tensor_us']} us, evict+remap 1.5 GB {vl['evict_remap_1p5gb_ms']} ms")
     t = r.get("turbo")
     if t:
         for mode in ("engine_layout", "reference_layout"):

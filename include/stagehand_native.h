@@ -547,6 +547,12 @@ int sh_vmm_create_slab(sh_vmm* v, uint64_t size, uint32_t* slab);               
 int sh_vmm_define_region(sh_vmm* v, uint32_t slab, uint64_t offset, uint64_t size, uint32_t* region); /* :175-198 */
 int sh_vmm_ensure_resident(sh_vmm* v, uint32_t slab, uint32_t region, void* stream, sh_vmm_handle** out); /* :213-468 */
 int sh_vmm_prefetch(sh_vmm* v, uint32_t slab, uint32_t region);                 /* allocator.rs:470-503 */
+/* Times the fast path natively: out2[0] = ns per ensure_resident of a resident region (the
+ * handles released after the timed loop), out2[1] = ns per ensure_resident + handle release
+ * (which records an event on `stream`), each over `iters` calls. No reference counterpart:
+ * it measures the operation the reference publishes as "ensure_resident (hot path) 250 ns
+ * median" (README.md:165-170) without Python in the loop. */
+int sh_vmm_time_fast_path(sh_vmm* v, uint32_t slab, uint32_t region, void* stream, uint32_t iters, double* out2);
 int sh_vmm_set_priority(sh_vmm* v, uint32_t slab, uint32_t priority);          /* allocator.rs:505-533 */
 int sh_vmm_set_ceiling(sh_vmm* v, uint64_t ceiling_bytes);                      /* allocator.rs:535-537 */
 int sh_vmm_destroy_slab(sh_vmm* v, uint32_t slab);                              /* allocator.rs:539-585 */

@@ -197,6 +197,7 @@ _SIGNATURES: dict[str, list] = {
     "sh_turbo_set_timing": [_vp, _i32],
     "sh_vmm_create": [_i32, ctypes.c_uint64, ctypes.POINTER(_vp)],
     "sh_vmm_destroy": [_vp],
+    "sh_vmm_time_fast_path": [_vp, _u32, _u32, _vp, _u32, _vp],
     "sh_vmm_info": [_vp, _vp],
     "sh_vmm_create_slab": [_vp, ctypes.c_uint64, ctypes.POINTER(_u32)],
     "sh_vmm_define_region": [_vp, _u32, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(_u32)],

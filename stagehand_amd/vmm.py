@@ -120,6 +120,13 @@ class SlabAllocator:
     def prefetch(self, slab: int, region: int) -> None:
         _native.call("sh_vmm_prefetch", self._handle(), int(slab), int(region))
 
+    def time_fast_path(self, slab: int, region: int, stream: int, iters: int = 100_000) -> tuple[float, float]:
+        """Native timing of ensure_resident on a resident region: (ns per call with the handles
+        released after the loop, ns per call + release)."""
+        out = (ctypes.c_double * 2)()
+        _native.call("sh_vmm_time_fast_path", self._handle(), int(slab), int(region), int(stream), int(iters), out)
+        return out[0], out[1]
+
     def set_priority(self, slab: int, priority: int) -> None:
         _native.call("sh_vmm_set_priority", self._handle(), int(slab), int(priority))
 
