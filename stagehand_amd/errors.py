@@ -16,20 +16,20 @@ __all__ = [
 
 
 class StagehandError(Exception):
-    """Base exception for all stagehand errors."""
+    """Root of every error this package raises on purpose."""
 
 
 class StagehandOOMError(StagehandError):
-    """Block too large for the pinned pool."""
+    """A block (or a request of slabs) does not fit the pinned slab pool."""
 
 
 class DtypeMismatchError(StagehandError):
-    """Strict bf16 enforcement violation."""
+    """A block produced a dtype other than bf16 while strict bf16 checking is on."""
 
 
 class InvalidStateTransitionError(StagehandError):
-    """Illegal residency state machine transition."""
+    """A block was asked to move between residency states the FSM does not connect."""
 
 
 class TransferError(StagehandError):
-    """Async H2D/D2H copy failure."""
+    """A host-to-device or device-to-host copy failed in the native engine."""

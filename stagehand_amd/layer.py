@@ -118,8 +118,9 @@ class LayerRuntime:
         self._inference_mode = inference_mode
         layers = _discover_layers(model)
         if not layers:
-            raise ValueError("No eligible layers found (nn.Linear, nn.Conv2d, nn.Embedding). "
-                             "Model must contain at least one parameterized layer.")
+            # the message starts as the reference's does: callers match on "No eligible layers"
+            raise ValueError("No eligible layers in the model: layer mode streams nn.Linear, nn.Conv2d and "
+                             "nn.Embedding modules, and it found none with parameters.")
         self._layer_map: dict[str, nn.Module] = dict(layers)
         self._all_layer_names = [n for n, _ in layers]
         self._config = _auto_pool_config(layers, dtype, prefetch_k, _parse_budget(vram_budget), _parse_budget(ram_budget))
@@ -156,7 +157,7 @@ class LayerRuntime:
         self._mode = "trace"
         self._install_hooks(self._registry_order(), trace=True)
         _native.track(self, _native.CLOSE_RUNTIME, "shutdown")
-        log.info("LayerRuntime: %d layers discovered, pool=%dMB (%dMB slabs), prefetch_k=%d, mode=trace",
+        log.info("layer mode: tracing %d layers; pinned pool %d MB in %d MB slabs; prefetch_k=%d",
                  len(layers), self._config.pinned_pool_mb, self._config.pinned_slab_mb, prefetch_k)
 
     def _new_scheduler(self, prefetch_window: int) -> StagehandScheduler:
@@ -257,8 +258,8 @@ class LayerRuntime:
         self._scheduler.begin_step(self._step)
         self._forward_started = True
         self._mode = "scheduled"
-        log.info("LayerRuntime: trace complete (%d layers), rebuilding with prefetch_k=%d", len(self._trace_order),
-                 self._prefetch_k)
+        log.info("layer mode: traced %d layers in execution order; scheduling them with prefetch_k=%d",
+                 len(self._trace_order), self._prefetch_k)
 
     def _remove_hooks(self) -> None:
         for h in self._hook_handles:
@@ -284,7 +285,7 @@ class LayerRuntime:
 
     def shutdown_keep_pool(self) -> PinnedPool:
         if self._mode == "shutdown":
-            raise RuntimeError("Already shut down")
+            raise RuntimeError("this layer runtime has been shut down")
         self._remove_hooks()
         self._engine.shutdown()
         self._scheduler.close()
