@@ -553,15 +553,22 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     timeline = timeline_stats(rt.engine.stop_trace(), getattr(args, "pcie_peak_gbps", None))
     check = None
     if layers is not None:
-        # a resident block's streamed weight against the torch device dequant of its payload
-        for e in rt.registry.blocks_in_order()[::-1]:
-            if rt.residency.get_entry(e.block_id).gpu_tensor is not None:
-                blk = e.module_ref()
-                name, lin = next((f"{e.block_id}.{n}", m) for n, m in blk.named_modules() if isinstance(m, torch.nn.Linear))
-                L = layers[name]
-                want = (L["qweight"].cuda().to(torch.float32) * L["scale"].cuda().unsqueeze(1)).to(torch.bfloat16)
-                check = {"layer": name, "bit_exact": bool(torch.equal(lin.weight.view(torch.int16), want.view(torch.int16)))}
-                break
+        # every Linear of every resident block: its streamed weight and bias against the torch
+        # device expression of the reference's host dequant (scheduler.py:290-308) on its payload
+        n_layers, exact = 0, True
+        for e in rt.registry.blocks_in_order():
+            if rt.residency.get_entry(e.block_id).gpu_tensor is None:
+                continue
+            for n, lin in e.module_ref().named_modules():
+                if not isinstance(lin, torch.nn.Linear):
+                    continue
+                L = layers[f"{e.block_id}.{n}"]
+                want = ((L["qweight"].cuda().to(torch.float32) - L["zero_point"].cuda().unsqueeze(1))
+                        * L["scale"].cuda().unsqueeze(1)).to(torch.bfloat16)
+                exact &= bool(torch.equal(lin.weight.view(torch.int16), want.view(torch.int16)))
+                exact &= bool(torch.equal(lin.bias.view(torch.int16), L["bias"].cuda().to(torch.bfloat16).view(torch.int16)))
+                n_layers += 1
+        check = {"resident_layers_checked": n_layers, "bit_exact": exact}
     res = {
         "source_mode": "pinned source images" if pinned else "bounded pinned pool (staged)",
         "file_reader": reader if kind in ("file", "squareq_v2") else None,
@@ -1581,6 +1588,9 @@ def summary_line(r: dict) -> str:
         if tl:
             parts[-1] += (f", copying {tl.get('h2d_gbps_while_copying')} GB/s, "
                           f"compute hidden {tl.get('compute_hidden_frac')}")
+        wc = best.get("weight_check") if isinstance(best, dict) else None
+        if isinstance(wc, dict) and "resident_layers_checked" in wc:
+            parts[-1] += f", weights bit-exact {wc['bit_exact']} on {wc['resident_layers_checked']} resident layers"
         ref = d.get("reference_host_dequant_path")
         if ref:
             parts.append(f"{label} reference host path {ref['ms_per_step']} ms/step on {ref['cores']} cores")
