@@ -687,6 +687,32 @@ def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | Non
     return out
 
 
+def kernel_stats(trace_dir: Path, skip: int) -> dict:
+    """Per-kernel dispatch statistics of a rocprofv3 ``--kernel-trace`` CSV for the library's kernels
+    (``sh_*``), over the dispatches after the first ``skip`` of each kernel (the bench's warm-up
+    launches), in µs."""
+    import csv
+    import statistics
+
+    files = sorted(trace_dir.rglob("*kernel_trace.csv"))
+    if not files:
+        raise FileNotFoundError(f"no kernel_trace.csv under {trace_dir}")
+    per: dict[str, list[tuple[int, float]]] = {}
+    with open(files[0], newline="") as fh:
+        for row in csv.DictReader(fh):
+            name = row["Kernel_Name"]
+            if name.startswith("sh_"):
+                per.setdefault(name, []).append((int(row["Start_Timestamp"]),
+                                                 (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3))
+    out = {}
+    for name, rows in sorted(per.items()):
+        d = [us for _t, us in sorted(rows)][skip:]
+        if d:
+            out[name] = {"calls": len(d), "avg_us": round(statistics.fmean(d), 2), "min_us": round(min(d), 2),
+                         "max_us": round(max(d), 2), "median_us": round(statistics.median(d), 2)}
+    return out
+
+
 def pmc_summary(dirs: list[Path]) -> dict:
     """Per-kernel medians of every counter in rocprofv3 ``--pmc`` CSVs (``*counter_collection.csv``
     under each directory), for the library's kernels (names starting with ``sh_``), with the
@@ -1365,6 +1391,9 @@ def main() -> int:
     ap.add_argument("--trace-summary", default=None, metavar="DIR",
                     help="only summarise the copy/compute overlap of a rocprofv3 CSV trace in DIR (no GPU)")
     ap.add_argument("--trace-bytes", type=int, default=None, help="H2D bytes inside the marked window")
+    ap.add_argument("--kernel-stats", default=None, metavar="DIR",
+                    help="only print per-kernel dispatch statistics of a rocprofv3 kernel trace in DIR (no GPU); "
+                         "the first --warmup dispatches of each kernel are left out")
     ap.add_argument("--pmc-summary", nargs="+", default=None, metavar="DIR",
                     help="only print per-kernel medians of rocprofv3 --pmc CSVs under DIRs (no GPU)")
     ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
@@ -1378,6 +1407,9 @@ def main() -> int:
 
     if args.trace_summary:
         print(json.dumps(trace_summary(Path(args.trace_summary), args.trace_bytes, args.pcie_gbps)), flush=True)
+        return 0
+    if args.kernel_stats:
+        print(json.dumps(kernel_stats(Path(args.kernel_stats), args.warmup), indent=1), flush=True)
         return 0
     if args.pmc_summary:
         print(json.dumps(pmc_summary([Path(d) for d in args.pmc_summary]), indent=1), flush=True)
