@@ -500,9 +500,14 @@ def timeline_stats(trace: dict, pcie_peak_gbps: float | None) -> dict:
         d2h_iv = _union([(a, b) for _n, a, b, *_k in d2h])
         d2h_ms = _length(d2h_iv)
         res["d2h_busy_ms"] = round(d2h_ms, 2)
+        res["d2h_busy_frac"] = round(d2h_ms / (span1 - span0), 4)
         res["d2h_gbps_while_copying"] = round(sum(d[0] for d in d2h) / (d2h_ms * 1e-3) / 1e9, 2) if d2h_ms else None
         res["d2h_h2d_overlap_ms"] = round(_intersect(d2h_iv, copy_iv), 2)
         res["d2h_span_ms"] = [round(min(d[1] for d in d2h) - span0, 1), round(max(d[2] for d in d2h) - span0, 1)]
+    waits = trace.get("host_waits") or []
+    if waits:
+        res["host_waits"] = len(waits)
+        res["host_wait_ms"] = round(sum(b - a for _k, a, b in waits), 2)
     return res
 
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 4
+#define SH_ABI_VERSION 5
 
 enum sh_status {
   SH_OK = 0,
@@ -482,8 +482,10 @@ int sh_turbo_set_writeback(sh_turbo* t, uint32_t block, int enable);
 /* No reference counterpart: before sh_turbo_initialize, where write-backs run.
  * 1 (the default): on an SDMA engine (sh_saveback); a prefetch that reuses the
  * slot of a block being written back, or reloads that block, waits for the copy
- * on the host. 0: hipMemcpyAsync on the engine's evict stream (a kernel on the
- * compute units), ordered on the device only. */
+ * on the host (sh_turbo_step's lookahead prefetch leaves that wait, and its
+ * copy, to the next engine call, with the block already marked h2d). 0:
+ * hipMemcpyAsync on the engine's evict stream (a kernel on the compute units),
+ * ordered on the device only. */
 int sh_turbo_set_save_back(sh_turbo* t, int sdma);
 int sh_turbo_block_slot(sh_turbo* t, uint32_t block, int32_t* slot);     /* -1: none, engine.rs:375-378 */
 int sh_turbo_block_location(sh_turbo* t, uint32_t block, int* location); /* engine.rs:384-393 */
@@ -496,6 +498,22 @@ int sh_turbo_bytes(sh_turbo* t, uint64_t* h2d, uint64_t* d2h);
  * recorded earlier). */
 int sh_turbo_set_timing(sh_turbo* t, int enable);
 int sh_turbo_block_times(sh_turbo* t, uint32_t block, void* ref_event, float* out2);
+/* Spans recorded since timing was last switched on (no reference counterpart),
+ * on the HSA system clock of sh_saveback_clock_ns:
+ *   SH_TURBO_SPAN_WRITEBACK  a block's write-back on the SDMA engine, from the
+ *                            start of its first copy to the end of its last
+ *                            (both 0 when a tool replaced the copies' signals);
+ *   SH_TURBO_SPAN_HOST_WAIT  a host wait inside sh_turbo_step for the write-back
+ *                            out of the slot or pinned region a prefetch reuses.
+ * Waits for every recorded write-back first, copies up to `cap` spans to `out`
+ * and sets *n to the number recorded. */
+enum sh_turbo_span_kind { SH_TURBO_SPAN_WRITEBACK = 0, SH_TURBO_SPAN_HOST_WAIT = 1 };
+typedef struct sh_turbo_span {
+  uint32_t block, kind;
+  uint64_t start_ns, end_ns;
+  uint64_t bytes;  /* write-back bytes; 0 for a host wait */
+} sh_turbo_span;
+int sh_turbo_trace_spans(sh_turbo* t, sh_turbo_span* out, uint32_t cap, uint32_t* n);
 
 /* ───────────────────────── VMM residency allocator ─────────────────────────
  * Slabs of reserved device address space whose regions get physical memory on

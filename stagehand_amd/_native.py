@@ -214,6 +214,7 @@ _SIGNATURES: dict[str, list] = {
     "sh_vmm_handle_export": [_vp, ctypes.c_uint8, ctypes.c_uint8, ctypes.c_int32, _vp, ctypes.POINTER(_vp)],
     "sh_dl_free": [_vp],
     "sh_turbo_block_times": [_vp, _u32, _vp, _vp],
+    "sh_turbo_trace_spans": [_vp, _vp, _u32, _vp],
 }
 
 # Mirror of `struct sh_load_request`.
@@ -245,8 +246,11 @@ VMM_REGION_DTYPE = np.dtype([("state", "<u4"), ("refcount", "<u4"), ("offset", "
 
 # Mirror of `struct sh_copy_item`.
 COPY_ITEM_DTYPE = np.dtype([("dst", "<u8"), ("src", "<u8"), ("bytes", "<u8")])
+TURBO_SPAN_DTYPE = np.dtype([("block", "<u4"), ("kind", "<u4"), ("start_ns", "<u8"), ("end_ns", "<u8"),
+                             ("bytes", "<u8")])
+TURBO_SPAN_WRITEBACK, TURBO_SPAN_HOST_WAIT = 0, 1
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

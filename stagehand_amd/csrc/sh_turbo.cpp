@@ -24,7 +24,15 @@
 //    many times slower. A prefetch that reuses the slot of a block being
 //    written back, or reloads that block, then waits for the copy on the host
 //    (an SDMA copy has no device-side wait). Tickets complete in order, so
-//    the engine tracks the highest one known complete and releases the rest.
+//    the engine tracks the highest one known complete and releases the rest;
+//  * step()'s lookahead prefetch does not make that host wait: a copy that
+//    would wait is deferred to the next engine call (the block is marked h2d
+//    with its slot taken, as the reference's step leaves it). The caller
+//    queues the current block's compute first, and the write-back of that
+//    block can start as soon as the one before it ends. In a forward-only
+//    pass the last block keeps its slot, so a window of 3 rotates through 2
+//    slots, and waiting in step() would hold every block's compute behind
+//    the previous block's write-back.
 #include <algorithm>
 #include <deque>
 #include <mutex>
@@ -53,6 +61,12 @@ struct Block {
   bool timed = false;
 };
 
+// A queued write-back ticket and, in timing mode, the span that records its copy times.
+struct Pending {
+  uint64_t ticket;
+  int64_t span;  // index into sh_turbo::spans, -1: none
+};
+
 struct Slot {
   std::vector<void*> ptrs;      // per-parameter mode (reference layout)
   std::vector<uint64_t> sizes;  // per-position capacity in per-parameter mode
@@ -77,11 +91,14 @@ struct sh_turbo {
   hipEvent_t compute_mark = nullptr;
   sh_saveback* sb = nullptr;      // write-backs on an SDMA engine (null: on the evict stream)
   bool sdma = true;               // sh_turbo_set_save_back
-  std::deque<uint64_t> tickets;   // write-back tickets not yet released, in order
+  std::deque<Pending> tickets;    // write-back tickets not yet released, in order
+  int64_t deferred = -1;          // a lookahead block marked h2d whose copy is not issued yet
+  bool deferred_from_d2h = false; // ... and that was being written back itself
   uint64_t done_upto = 0;         // every ticket <= this one is complete (and released)
   int device = 0;
   bool initialized = false;
   bool timing = false;
+  std::vector<sh_turbo_span> spans;  // write-backs and host waits recorded in timing mode
   uint64_t bytes_h2d = 0, bytes_d2h = 0;
 };
 
@@ -159,10 +176,20 @@ int copy_block(sh_turbo* t, const Block& b, const Slot& s, bool to_device, hipSt
 // Releases the write-back tickets that have completed (they complete in order).
 int reap_tickets(sh_turbo* t) {
   while (!t->tickets.empty()) {
-    const uint64_t tk = t->tickets.front();
+    const uint64_t tk = t->tickets.front().ticket;
+    const int64_t span = t->tickets.front().span;
     int st = sh_saveback_query(t->sb, tk);
     if (st == SH_ERR_NOT_READY) break;
     if (st != SH_OK) return st;
+    if (span >= 0) {
+      // the copy engine's own start and end; none when a tool replaced the copies' signals
+      uint64_t times[2] = {0, 0};
+      if (sh_saveback_ticket_times(t->sb, tk, times) == SH_OK) {
+        t->spans[(size_t)span].start_ns = times[0];
+        t->spans[(size_t)span].end_ns = times[1];
+      }
+      sh::clear_error();
+    }
     t->done_upto = tk;
     t->tickets.pop_front();
     st = sh_saveback_release(t->sb, tk);
@@ -178,10 +205,18 @@ bool ticket_done(sh_turbo* t, uint64_t tk) {
 }
 
 // Host wait for a write-back ticket (and every earlier one), then releases them.
-int wait_ticket(sh_turbo* t, uint64_t tk) {
+// In timing mode a wait for block b is recorded as a host-wait span.
+int wait_ticket(sh_turbo* t, uint64_t tk, int64_t b = -1) {
   if (tk == 0 || tk <= t->done_upto) return SH_OK;
+  uint64_t t0 = 0;
+  if (t->timing && b >= 0 && sh_saveback_clock_ns(&t0) != SH_OK) t0 = 0;
   int st = sh_saveback_wait(t->sb, tk);
   if (st != SH_OK) return st;
+  if (t0 != 0) {
+    uint64_t t1 = 0;
+    if (sh_saveback_clock_ns(&t1) == SH_OK)
+      t->spans.push_back({(uint32_t)b, SH_TURBO_SPAN_HOST_WAIT, t0, t1, 0});
+  }
   return reap_tickets(t);
 }
 
@@ -235,17 +270,15 @@ int take_slot(sh_turbo* t, uint32_t b, int* out) {
   return SH_OK;
 }
 
-int async_prefetch(sh_turbo* t, uint32_t b) {
+// Issues the H2D of block b into its assigned slot on the prefetch stream.
+int issue_prefetch(sh_turbo* t, uint32_t b, bool from_d2h) {
   Block& blk = t->blocks[b];
-  if (blk.location == SH_TURBO_GPU || blk.location == SH_TURBO_H2D) return SH_OK;
-  int si = -1;
-  int rc = take_slot(t, b, &si);
-  if (rc != SH_OK) return rc;
-  Slot& s = t->slots[si];
+  Slot& s = t->slots[blk.slot];
+  int rc = SH_OK;
   // the pinned region may still be the target of this block's write-back
-  if (blk.location == SH_TURBO_D2H) {
+  if (from_d2h) {
     SH_HIP(hipStreamWaitEvent(t->prefetch, blk.d2h, 0));
-    rc = wait_ticket(t, blk.d2h_ticket);
+    rc = wait_ticket(t, blk.d2h_ticket, b);
     if (rc != SH_OK) return rc;
     blk.d2h_ticket = 0;
   }
@@ -254,7 +287,7 @@ int async_prefetch(sh_turbo* t, uint32_t b) {
     s.fenced = false;
   }
   // the slot may still be the source of the previous block's write-back
-  rc = wait_ticket(t, s.fence_ticket);
+  rc = wait_ticket(t, s.fence_ticket, b);
   if (rc != SH_OK) return rc;
   s.fence_ticket = 0;
   if (t->timing) SH_HIP(hipEventRecord(blk.t_start, t->prefetch));
@@ -267,6 +300,37 @@ int async_prefetch(sh_turbo* t, uint32_t b) {
   SH_HIP(hipEventRecord(blk.h2d, t->prefetch));
   blk.location = SH_TURBO_H2D;
   return SH_OK;
+}
+
+// Issues a deferred lookahead copy (waiting on the host for the write-back it follows).
+int flush_deferred(sh_turbo* t) {
+  if (t->deferred < 0) return SH_OK;
+  const uint32_t b = (uint32_t)t->deferred;
+  t->deferred = -1;
+  return issue_prefetch(t, b, t->deferred_from_d2h);
+}
+
+// Starts the H2D of block b into a free slot. With may_defer, a copy that would
+// first wait on the host for a write-back out of the slot (or out of the block's
+// own pinned region) is not issued yet: the block is marked h2d with its slot
+// assigned, and the next engine call issues it. Within step() that lets the
+// caller queue the current block's compute before the host blocks, so the
+// write-back engine is not left waiting for that compute.
+int async_prefetch(sh_turbo* t, uint32_t b, bool may_defer = false) {
+  Block& blk = t->blocks[b];
+  if (blk.location == SH_TURBO_GPU || blk.location == SH_TURBO_H2D) return SH_OK;
+  int si = -1;
+  int rc = take_slot(t, b, &si);
+  if (rc != SH_OK) return rc;
+  const bool from_d2h = blk.location == SH_TURBO_D2H;
+  if (may_defer && t->deferred < 0 &&
+      !(ticket_done(t, t->slots[si].fence_ticket) && (!from_d2h || ticket_done(t, blk.d2h_ticket)))) {
+    t->deferred = b;
+    t->deferred_from_d2h = from_d2h;
+    blk.location = SH_TURBO_H2D;
+    return SH_OK;
+  }
+  return issue_prefetch(t, b, from_d2h);
 }
 
 // Evicts block b after the compute marked in t->compute_mark (recorded by the
@@ -287,7 +351,14 @@ int async_evict(sh_turbo* t, uint32_t b) {
     std::vector<sh_copy_item> items = writeback_items(t, blk, s);
     int rc = sh_saveback_submit(t->sb, items.data(), items.size(), t->evict, &ticket);
     if (rc != SH_OK) return rc;
-    t->tickets.push_back(ticket);
+    int64_t span = -1;
+    if (t->timing) {
+      uint64_t bytes = 0;
+      for (const sh_copy_item& it : items) bytes += it.bytes;
+      span = (int64_t)t->spans.size();
+      t->spans.push_back({b, SH_TURBO_SPAN_WRITEBACK, 0, 0, bytes});
+    }
+    t->tickets.push_back({ticket, span});
   } else if (blk.writeback) {
     int rc = copy_block(t, blk, s, false, t->evict);
     if (rc != SH_OK) return rc;
@@ -319,7 +390,7 @@ int sync_prefetch(sh_turbo* t, uint32_t b, hipStream_t compute) {
 int sync_evict(sh_turbo* t) {
   SH_HIP(hipStreamSynchronize(t->evict));
   if (!t->tickets.empty()) {
-    int rc = wait_ticket(t, t->tickets.back());
+    int rc = wait_ticket(t, t->tickets.back().ticket);
     if (rc != SH_OK) return rc;
   }
   for (Block& blk : t->blocks) {
@@ -476,19 +547,34 @@ extern "C" int sh_turbo_step(sh_turbo* t, uint32_t block, int direction, void* c
   // the previous block's last kernels are queued now; mark them before the
   // compute stream is made to wait for this block's H2D
   SH_HIP(hipEventRecord(t->compute_mark, compute));
-  rc = sync_prefetch(t, block, compute);
-  if (rc != SH_OK) return rc;
   const uint32_t n = (uint32_t)t->blocks.size();
   const bool fwd = direction == SH_TURBO_FORWARD;
   const int64_t prev = fwd ? (int64_t)block - 1 : (int64_t)block + 1;
   const int64_t next = fwd ? (int64_t)block + 1 : (int64_t)block - 1;
-  if (prev >= 0 && prev < n) {
-    rc = async_evict(t, (uint32_t)prev);
+  const bool has_prev = prev >= 0 && prev < n;
+  if (t->deferred == (int64_t)block) {
+    // this block's copy was deferred behind a write-back: queue the previous
+    // block's write-back first, so the copy engine has it before the host
+    // wait in the deferred copy ends (the block already holds its slot)
+    if (has_prev) {
+      rc = async_evict(t, (uint32_t)prev);
+      if (rc != SH_OK) return rc;
+    }
+    rc = flush_deferred(t);
+    if (rc == SH_OK) rc = sync_prefetch(t, block, compute);
     if (rc != SH_OK) return rc;
+  } else {
+    rc = flush_deferred(t);
+    if (rc == SH_OK) rc = sync_prefetch(t, block, compute);
+    if (rc != SH_OK) return rc;
+    if (has_prev) {
+      rc = async_evict(t, (uint32_t)prev);
+      if (rc != SH_OK) return rc;
+    }
   }
   if (next >= 0 && next < n) {
     // no slot for the lookahead block is not an error (engine.rs:334-337)
-    if (async_prefetch(t, (uint32_t)next) != SH_OK) sh::clear_error();
+    if (async_prefetch(t, (uint32_t)next, true) != SH_OK) sh::clear_error();
   }
   return SH_OK;
 }
@@ -502,7 +588,8 @@ extern "C" int sh_turbo_evict_sync(sh_turbo* t, uint32_t block, void* compute_st
   if (rc != SH_OK) return rc;
   SH_HIP(hipSetDevice(t->device));
   SH_HIP(hipEventRecord(t->compute_mark, static_cast<hipStream_t>(compute_stream)));
-  rc = async_evict(t, block);
+  rc = flush_deferred(t);
+  if (rc == SH_OK) rc = async_evict(t, block);
   if (rc != SH_OK) return rc;
   return sync_evict(t);
 }
@@ -513,7 +600,8 @@ extern "C" int sh_turbo_drain(sh_turbo* t) {
   std::lock_guard<std::mutex> g(t->mu);
   if (!t->initialized) return SH_OK;
   SH_HIP(hipSetDevice(t->device));
-  int rc = sync_evict(t);
+  int rc = flush_deferred(t);
+  if (rc == SH_OK) rc = sync_evict(t);
   if (rc != SH_OK) return rc;
   SH_HIP(hipStreamSynchronize(t->prefetch));
   return SH_OK;
@@ -654,8 +742,31 @@ extern "C" int sh_turbo_set_timing(sh_turbo* t, int enable) {
       if (!b.t_end) SH_HIP(hipEventCreate(&b.t_end));
       b.timed = false;
     }
+    if (t->sb) {
+      rc = sh_saveback_set_timing(t->sb, 1);
+      if (rc != SH_OK) return rc;
+    }
+    t->spans.clear();
   }
   t->timing = enable != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_turbo_trace_spans(sh_turbo* t, sh_turbo_span* out, uint32_t cap, uint32_t* n) {
+  sh::clear_error();
+  if (!t || !n || (cap && !out)) return sh::fail(SH_ERR_INVALID, "sh_turbo_trace_spans: null argument");
+  std::lock_guard<std::mutex> g(t->mu);
+  int rc = require_init(t);
+  if (rc != SH_OK) return rc;
+  // every recorded write-back has completed before its times are read
+  for (auto it = t->tickets.rbegin(); it != t->tickets.rend(); ++it) {
+    if (it->span < 0) continue;
+    rc = wait_ticket(t, it->ticket);
+    if (rc != SH_OK) return rc;
+    break;
+  }
+  *n = (uint32_t)t->spans.size();
+  std::copy_n(t->spans.begin(), std::min<size_t>(cap, t->spans.size()), out);
   return SH_OK;
 }
 

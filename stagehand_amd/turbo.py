@@ -165,6 +165,16 @@ class TransferEngine:
         _native.call("sh_turbo_block_times", self._handle(), int(block_idx), ref_event.handle, out)
         return out[0], out[1]
 
+    def trace_spans(self):
+        """Write-back and host-wait spans recorded since timing was switched on (a numpy array
+        of ``_native.TURBO_SPAN_DTYPE``, times on the save-back engine's HSA clock)."""
+        n = ctypes.c_uint32()
+        _native.call("sh_turbo_trace_spans", self._handle(), None, 0, ctypes.byref(n))
+        out = np.zeros(n.value, dtype=_native.TURBO_SPAN_DTYPE)
+        if n.value:
+            _native.call("sh_turbo_trace_spans", self._handle(), out.ctypes.data, n.value, ctypes.byref(n))
+        return out[:n.value]
+
     def drain(self) -> None:
         _native.call("sh_turbo_drain", self._handle())
 
@@ -228,6 +238,7 @@ class TurboConductor:
         self._cpu_tensors: list[list[torch.Tensor]] = []
         self._offsets: list[list[int]] = []
         self._trace_ref = None
+        self._trace_t0_ns = 0
         self._trace_compute: list = []
         self._trace_loaded: list[int] = []
         log.info("TurboConductor: %d blocks", len(self._block_modules))
@@ -328,12 +339,15 @@ class TurboConductor:
     def start_trace(self) -> None:
         """Time every later block H2D and the compute between before_block and after_block,
         relative to an event recorded now on the current stream."""
-        from stagehand_amd.transfer import NativeEvent
+        from stagehand_amd.transfer import NativeEvent, SaveBackEngine
 
         assert self._engine is not None
         self._engine.set_timing(True)
         self._trace_ref = NativeEvent(timing=True)
         self._trace_ref.record(torch.cuda.current_stream().cuda_stream)
+        # write-back and host-wait spans are on the HSA clock: read it when the reference event completes
+        self._trace_ref.synchronize()
+        self._trace_t0_ns = SaveBackEngine.clock_ns()
         self._trace_compute, self._trace_loaded = [], []
 
     def _trace_step_loads(self, block_idx: int, direction: str) -> None:
@@ -358,7 +372,9 @@ class TurboConductor:
                     break
 
     def stop_trace(self) -> dict:
-        """{"loads": [(block, bytes, start, end, end) ms], "compute": [(block, start, end) ms]}."""
+        """{"loads": [(block, bytes, start, end, end)], "compute": [(block, start, end)],
+        "d2h": [(bytes, start, end, "writeback")], "host_waits": [("slot_reuse", start, end)]}, in ms
+        after start_trace; "d2h_untimed" counts write-backs without copy times."""
         if self._trace_ref is None:
             return {"loads": [], "compute": []}
         torch.cuda.synchronize()
@@ -369,10 +385,20 @@ class TurboConductor:
             loads.append((self._block_names[b], sum(m[2] for m in self._param_meta[b]), t0, t1, t1))
         compute = [(self._block_names[b], ref.elapsed_ms(s), ref.elapsed_ms(e)) for b, s, e in self._trace_compute
                    if e is not None]
+        d2h, waits, untimed = [], [], 0
+        t0_ns = self._trace_t0_ns
+        for sp in self._engine.trace_spans():
+            start, end = (int(sp["start_ns"]) - t0_ns) / 1e6, (int(sp["end_ns"]) - t0_ns) / 1e6
+            if sp["kind"] == _native.TURBO_SPAN_HOST_WAIT:
+                waits.append(("slot_reuse", start, end))
+            elif sp["start_ns"] == 0:
+                untimed += 1
+            else:
+                d2h.append((int(sp["bytes"]), start, end, "writeback"))
         self._engine.set_timing(False)
         self._trace_ref = None
         self._trace_compute, self._trace_loaded = [], []
-        return {"loads": loads, "compute": compute}
+        return {"loads": loads, "compute": compute, "d2h": d2h, "d2h_untimed": untimed, "host_waits": waits}
 
     def install_hooks(self) -> list:
         """Forward pre/post hooks that call before_block / after_block (not in the reference)."""

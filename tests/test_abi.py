@@ -71,6 +71,7 @@ def test_struct_mirrors_match_the_c_layout(tmp_path):
         "sh_pool_stats": _native.POOL_STATS_DTYPE,
         "sh_vmm_stats": _native.VMM_STATS_DTYPE,
         "sh_vmm_region_stats": _native.VMM_REGION_DTYPE,
+        "sh_turbo_span": _native.TURBO_SPAN_DTYPE,
     }
     lines = ['#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {"]
     for struct, dt in mirrors.items():

@@ -270,3 +270,105 @@ def test_conductor_with_writeback_and_other_windows_matches_resident_model(windo
     cond.shutdown()
     for p, q in zip(model.parameters(), ref.parameters()):
         assert torch.equal(p.view(torch.int16), q.cpu().view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_trace_records_every_write_back_and_host_wait():
+    """A traced pass with write-back of every block in the reference's per-parameter layout: one
+    write-back span per evicted block with the block's bytes, timed by the copy engine after that
+    block's compute began, and host waits that end after they start."""
+    model = init_(TinyStack(n=6, hidden=64, mlp=4), seed=9).to(torch.bfloat16)
+    model.requires_grad_(False)
+    x = torch.randn(8, 64, generator=torch.Generator().manual_seed(10)).to("cuda", torch.bfloat16)
+    cond = TurboConductor(model, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, writeback="always",
+                          contiguous_slots=False)
+    cond.prepare()
+    handles = cond.install_hooks()
+    with torch.no_grad():
+        model(x)
+        torch.cuda.synchronize()
+        cond.start_trace()
+        model(x)
+        trace = cond.stop_trace()
+    # step(i) evicts block i-1: blocks 0-4 are written back during the pass, block 5 keeps its slot
+    assert trace["d2h_untimed"] == 0
+    assert len(trace["d2h"]) == 5
+    block_bytes = sum(p.numel() * 2 for p in model.blocks[0].parameters())
+    starts = {name: s for name, s, _e in trace["compute"]}
+    for k, (nbytes, t0, t1, kind) in enumerate(trace["d2h"]):
+        assert kind == "writeback" and nbytes == block_bytes
+        assert 0 < t0 <= t1
+        # the copy engine's clock and the HIP timeline are aligned to within a millisecond here
+        assert t0 >= starts[f"blocks.{k}"] - 1.0
+    for kind, t0, t1 in trace["host_waits"]:
+        assert kind == "slot_reuse" and t0 <= t1
+    for h in handles:
+        h.remove()
+    cond.shutdown()
+
+
+def _sleep_cycles_for(ms: float) -> int:
+    """Cycles of torch.cuda._sleep (a bounded spin kernel) that keep the current stream busy for
+    about ``ms`` milliseconds on this device."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    probe = 1_000_000
+    torch.cuda._sleep(probe)  # first launch loads the kernel
+    start.record()
+    torch.cuda._sleep(probe)
+    end.record()
+    end.synchronize()
+    per_ms = probe / max(start.elapsed_time(end), 1e-3)
+    return int(min(per_ms * ms, 4_000_000_000))
+
+
+@pytest.mark.gpu
+def test_lookahead_behind_a_write_back_is_issued_by_the_next_step():
+    """When every free slot is still the source of a write-back waiting for queued compute, step()
+    does not block the host on it: the lookahead block is marked h2d and the next step issues its
+    copy after the write-back. Every block still lands byte-exact and the write-back carries the
+    change made on the device."""
+    import time
+
+    sizes = lambda i: [(1 << 20) + 512 * i, 4096]
+    data = _blocks(5, 4, sizes)
+    e = TransferEngine()
+    for d in data:
+        e.register_block([t.numel() for t in d])
+    e.set_save_back("sdma")
+    e.initialize(torch.cuda.current_device(), 3)
+    for i, d in enumerate(data):
+        e.stage_block(i, [t.data_ptr() for t in d])
+    nb = e.slot_bytes()
+    slots = [torch.empty(nb, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    for s, t in enumerate(slots):
+        e.set_slot_buffer(s, t.data_ptr(), nb)
+    spin = _sleep_cycles_for(300.0)
+    e.set_timing(True)
+    e.step(0, "forward")            # block 0 into slot 0, lookahead 1 into slot 1
+    torch.cuda._sleep(spin)         # block 0's compute: both write-backs below wait for it
+    e.step(1, "forward")            # evicts 0; lookahead 2 takes the unused slot 2
+    base = slots[e.block_slot(1)]
+    base[e.param_offset(1, 0)] += 1
+    data[1][0][0] += 1
+    t0 = time.perf_counter()
+    e.step(2, "forward")            # evicts 1; lookahead 3 can only reuse slot 0 or 1
+    host_s = time.perf_counter() - t0
+    assert host_s < 0.15, f"step() waited {host_s * 1e3:.0f} ms for a write-back"
+    assert e.block_location(3) == "h2d"
+    e.step(3, "forward")            # issues block 3's copy once block 0's write-back is done
+    torch.cuda.synchronize()
+    base = slots[e.block_slot(3)]
+    for p, want in enumerate(data[3]):
+        off = e.param_offset(3, p)
+        assert torch.equal(base[off:off + want.numel()].cpu(), want), p
+    spans = e.trace_spans()
+    waits = spans[spans["kind"] == 1]
+    assert len(waits) >= 1 and all(int(w["block"]) == 3 for w in waits)
+    e.set_timing(False)
+    e.drain()
+    for i in range(3):
+        assert e.block_location(i) == "cpu"
+        for p, want in enumerate(data[i]):
+            buf = (ctypes.c_uint8 * want.numel()).from_address(e.cpu_ptr(i, p))
+            assert torch.equal(torch.frombuffer(buf, dtype=torch.uint8), want), (i, p)
+    e.close()
