@@ -424,6 +424,16 @@ int sh_saveback_create(int device, sh_saveback** out);
  * frees the engine; returns the first copy failure, if any. */
 int sh_saveback_destroy(sh_saveback* sb);
 int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream, uint64_t* ticket);
+/* As sh_saveback_submit, but the copies start once each of the n_events events
+ * (hipEvent_t) has completed, instead of after everything queued on a stream:
+ * the worker waits for each event on the host. The caller vouches that no work
+ * queued after those events writes the sources, and keeps the events alive, and
+ * does not record them again, until the ticket completes. An event recorded in
+ * the middle of a busy compute stream completes there: no stream is needed, so
+ * no hardware queue that the stream would share with that compute. No
+ * reference counterpart. */
+int sh_saveback_submit_after(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* const* events,
+                             uint32_t n_events, uint64_t* ticket);
 /* SH_OK when the ticket (and every earlier one) is complete, SH_ERR_NOT_READY
  * before, or the failure of a copy. */
 int sh_saveback_query(sh_saveback* sb, uint64_t ticket);

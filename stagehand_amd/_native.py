@@ -168,6 +168,7 @@ _SIGNATURES: dict[str, list] = {
     "sh_saveback_create": [_i32, ctypes.POINTER(_vp)],
     "sh_saveback_destroy": [_vp],
     "sh_saveback_submit": [_vp, _vp, ctypes.c_uint64, _vp, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_submit_after": [_vp, _vp, ctypes.c_uint64, _vp, _u32, ctypes.POINTER(ctypes.c_uint64)],
     "sh_saveback_query": [_vp, ctypes.c_uint64],
     "sh_saveback_wait": [_vp, ctypes.c_uint64],
     "sh_saveback_release": [_vp, ctypes.c_uint64],

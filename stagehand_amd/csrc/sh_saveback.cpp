@@ -13,7 +13,8 @@
 //
 // Ordering: an HSA copy cannot wait for a HIP event on the device, so each
 // submit records an event on the caller's stream and a worker thread waits
-// for it on the host before it issues the copies. Completion: each copy has an
+// for it on the host before it issues the copies (or, for
+// sh_saveback_submit_after, waits for the caller's own events). Completion: each copy has an
 // HSA signal of its own, initialised to 1, which the copy engine decrements. (HSA
 // lets several copies share one signal initialised to their count, but the
 // profiler's copy tracing replaces each copy's completion signal and forwards
@@ -50,6 +51,7 @@ namespace {
 struct Job {
   uint64_t id = 0;
   hipEvent_t fence = nullptr;  // none for a ticket without copies
+  std::vector<hipEvent_t> after;  // the caller's events (sh_saveback_submit_after), not owned
   std::vector<sh_copy_item> items;
   std::vector<hsa_signal_t> done;  // done[k]: 1 until items[k] has been copied
   int status = SH_OK;  // set (under the engine lock) before a failure completes the signals
@@ -115,7 +117,8 @@ void worker_loop(sh_saveback* sb) {
       j = sb->queue.front();
       sb->queue.pop_front();
     }
-    hipError_t e = hipEventSynchronize(j->fence);
+    hipError_t e = j->fence != nullptr ? hipEventSynchronize(j->fence) : hipSuccess;
+    for (size_t k = 0; e == hipSuccess && k < j->after.size(); ++k) e = hipEventSynchronize(j->after[k]);
     if (e != hipSuccess) {
       fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), 0);
       continue;
@@ -224,11 +227,12 @@ extern "C" int sh_saveback_destroy(sh_saveback* sb) {
   return first;
 }
 
-extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream,
-                                  uint64_t* ticket) {
-  sh::clear_error();
-  if (sb == nullptr || ticket == nullptr || (n > 0 && items == nullptr))
-    return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: NULL argument");
+namespace {
+
+// Queues a ticket whose copies wait for an event recorded now on `stream` (events == nullptr) or
+// for the caller's events.
+int submit_job(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream, void* const* events,
+               uint32_t n_events, uint64_t* ticket) {
   *ticket = 0;
   auto j = std::make_shared<Job>();
   for (uint64_t i = 0; i < n; ++i) {
@@ -247,7 +251,9 @@ extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, ui
   // A ticket without copies is complete at once (it has no signals): it gets no fence and
   // never reaches the worker, which only waits for fences and issues copies.
   const bool empty = j->items.empty();
-  if (!empty) {
+  if (!empty && events != nullptr) {
+    j->after.assign(reinterpret_cast<const hipEvent_t*>(events), reinterpret_cast<const hipEvent_t*>(events) + n_events);
+  } else if (!empty) {
     hipError_t e = hipEventCreateWithFlags(&j->fence, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(j->fence, (hipStream_t)stream);
     if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "sh_saveback_submit: fence event: %s", hipGetErrorString(e));
@@ -262,6 +268,28 @@ extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, ui
   if (!empty) sb->cv.notify_one();
   *ticket = j->id;
   return SH_OK;
+}
+
+}  // namespace
+
+extern "C" int sh_saveback_submit(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* stream,
+                                  uint64_t* ticket) {
+  sh::clear_error();
+  if (sb == nullptr || ticket == nullptr || (n > 0 && items == nullptr))
+    return sh::fail(SH_ERR_INVALID, "sh_saveback_submit: NULL argument");
+  return submit_job(sb, items, n, stream, nullptr, 0, ticket);
+}
+
+extern "C" int sh_saveback_submit_after(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* const* events,
+                                        uint32_t n_events, uint64_t* ticket) {
+  sh::clear_error();
+  if (sb == nullptr || ticket == nullptr || (n > 0 && items == nullptr) || (n_events > 0 && events == nullptr))
+    return sh::fail(SH_ERR_INVALID, "sh_saveback_submit_after: NULL argument");
+  for (uint32_t k = 0; k < n_events; ++k)
+    if (events[k] == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_submit_after: event %u is NULL", k);
+  static void* const kNone[1] = {nullptr};
+  // no events: nothing to wait for (an empty, non-null list marks the caller's-events form)
+  return submit_job(sb, items, n, nullptr, n_events ? events : kNone, n_events, ticket);
 }
 
 extern "C" int sh_saveback_query(sh_saveback* sb, uint64_t ticket) {

@@ -222,6 +222,14 @@ class StagehandScheduler:
         self._host_homes: dict[str, torch.Tensor] = {}
         # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
         self._done_marks: collections.deque = collections.deque()
+        # save-back fences (_save_back_fence): per module-backed block, an event after its last
+        # hook or gradient accumulation; an event where the step began; the blocks' parameter
+        # version counters then; the gradient-accumulation hooks that record those events
+        self._last_use: dict[str, Any] = {}
+        self._step_mark: Any = None
+        self._step_versions: dict[str, tuple[int, ...]] = {}
+        self._in_step = False
+        self._grad_hooks: list = []
         # device memory that an eviction gave up is left out of the budget while the
         # save-back copy still holds it (the reference's synchronous copy frees it at once)
         count_as_released = getattr(budget, "count_as_released", None)
@@ -241,8 +249,10 @@ class StagehandScheduler:
         self._cursor = 0
         self._backward_phase = False
         self._telemetry.begin_step(step)
+        self._mark_step_begin()
 
     def end_step(self) -> None:
+        self._remove_grad_hooks()
         self._backward_phase = False
         self._sync_d2h_fences()
         self._engine.reap()
@@ -270,6 +280,70 @@ class StagehandScheduler:
             if ev is not None:
                 with self._host_wait("d2h_fence"):
                     ev.synchronize()
+
+    # ── save-back fences ─────────────────────────────────────────────
+
+    def _module_backed_modules(self):
+        for entry in self._ordered_blocks:
+            if entry.file_backed or entry.squareq_backed or entry.eriquant_backed:
+                continue
+            module = entry.module_ref()
+            if module is not None:
+                yield entry.block_id, module
+
+    def _mark_step_begin(self) -> None:
+        """Records where the step began (after the previous step's optimizer) and the parameter
+        version counters of the module-backed blocks then, and hooks gradient accumulation of
+        their trainable parameters until end_step (for the save-back fences)."""
+        self._remove_grad_hooks()
+        record = getattr(self._engine, "record_event", None)
+        self._step_mark = record() if self._has_cuda and callable(record) else None
+        self._in_step = self._step_mark is not None
+        if not self._in_step:
+            return
+        self._step_versions = {}
+        for block_id, module in self._module_backed_modules():
+            params = list(module.parameters())
+            self._step_versions[block_id] = tuple(p._version for p in params)
+            hook = self._grad_hook_for(block_id)
+            self._grad_hooks.extend(p.register_post_accumulate_grad_hook(hook) for p in params if p.requires_grad)
+
+    def _grad_hook_for(self, block_id: str):
+        def hook(_param: torch.Tensor) -> None:
+            self._record_last_use(block_id)
+        return hook
+
+    def _record_last_use(self, block_id: str) -> None:
+        if self._in_step:
+            self._last_use[block_id] = self._engine.record_event()
+
+    def _save_back_fence(self, block_id: str, module: nn.Module | None) -> list | None:
+        """What a save-back of the block's parameters and gradients waits for before it starts:
+        a list of events, or None for everything queued on the current stream so far (the
+        reference's synchronous copy).
+
+        Inside a step, the work queued since the block's last hook and its last gradient
+        accumulation belongs to other blocks: it reads their parameters, not this block's. The
+        optimizer and other work between steps is before the step's start. So the copy needs only
+        those events, and the save-back engine need not wait for compute queued far ahead of it
+        (the host runs ahead of the device by up to max_run_ahead_blocks blocks). A parameter
+        changed in place since the step began (its version counter moved) takes the whole queue.
+        Writes through ``param.data`` do not move the counter and are not seen here."""
+        if not self._in_step or module is None:
+            return None
+        versions = self._step_versions.get(block_id)
+        if versions is None or versions != tuple(p._version for p in module.parameters()):
+            return None
+        last = self._last_use.get(block_id)
+        return [self._step_mark] if last is None else [last, self._step_mark]
+
+    def _remove_grad_hooks(self) -> None:
+        for h in self._grad_hooks:
+            h.remove()
+        self._grad_hooks.clear()
+        self._last_use.clear()
+        self._step_mark = None
+        self._in_step = False
 
     def _host_wait(self, kind: str):
         """The engine's host-wait accounting (a no-op context for engines without it)."""
@@ -299,8 +373,11 @@ class StagehandScheduler:
             return
         # a parameter viewing the block buffer is copied out of it on the device first, so the
         # buffer is not held until the save-back completes (it is freed when the block is dropped)
-        srcs = [t if t.untyped_storage().nbytes() <= t.numel() * t.element_size() else t.clone() for t in srcs]
-        outs, ev = self._engine.d2h_async(srcs)
+        views = [t.untyped_storage().nbytes() > t.numel() * t.element_size() for t in srcs]
+        srcs = [t.clone() if v else t for t, v in zip(srcs, views)]
+        # the clones are queued on the current stream now: then the copy waits for the whole queue
+        after = None if any(views) else self._save_back_fence(block_id, module)
+        outs, ev = self._engine.d2h_async(srcs, after=after)
         params = dict(module.named_parameters())
         for (what, name), out in zip(targets, outs):
             if what == "data":
@@ -336,7 +413,7 @@ class StagehandScheduler:
         if home is None or home.numel() < end:
             home = torch.empty(end, dtype=torch.uint8, pin_memory=True)
             self._host_homes[block_id] = home
-        ev = self._engine.d2h_into(base[:end], home[:end])
+        ev = self._engine.d2h_into(base[:end], home[:end], after=self._save_back_fence(block_id, module))
         _restore_params_from_tensor(module, home, layout)
         if ev is not None:
             self._d2h_fences[block_id] = ev
@@ -435,6 +512,7 @@ class StagehandScheduler:
 
     def close(self) -> None:
         self._sync_d2h_fences()
+        self._remove_grad_hooks()
         self._file_tensor_views.clear()
         for fh, mm, view in self._file_maps.values():
             for fn in (view.release, mm.close, fh.close):
@@ -521,6 +599,8 @@ class StagehandScheduler:
 
     def after_block(self, block_id: str, output: torch.Tensor | None = None) -> None:
         self._engine.mark_compute(block_id, start=False)
+        if self._in_step and block_id in self._step_versions:
+            self._record_last_use(block_id)
         self._mark_block_done()
         self._residency.decrement_ref(block_id)
         self._residency.get_entry(block_id).last_used_step = self._current_step

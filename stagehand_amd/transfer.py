@@ -120,6 +120,15 @@ class SaveBackEngine:
                      stream_handle, ctypes.byref(ticket))
         return SaveBackTicket(self, ticket.value)
 
+    def submit_after(self, items: np.ndarray, events: "list[NativeEvent]") -> "SaveBackTicket":
+        """Copies ``items`` once each of ``events`` has completed (the caller keeps them alive and
+        unrecorded until the ticket completes)."""
+        ticket = ctypes.c_uint64()
+        handles = (ctypes.c_void_p * max(1, len(events)))(*[ev.handle.value for ev in events])
+        _native.call("sh_saveback_submit_after", self.handle, items.ctypes.data if len(items) else None, len(items),
+                     handles, len(events), ctypes.byref(ticket))
+        return SaveBackTicket(self, ticket.value)
+
     def set_timing(self, enable: bool) -> None:
         _native.call("sh_saveback_set_timing", self.handle, int(enable))
         self._timing = bool(enable)
@@ -569,7 +578,9 @@ class AsyncTransferEngine:
 
     def stop_trace(self) -> dict:
         """Drains and returns {"loads": [(block, bytes, start, copied, done) ms], "compute": [(block, start,
-        end) ms], "d2h": [(bytes, start, end ms, "block" | "params")] (save-back copies)}."""
+        end) ms], "d2h": [(bytes, start, end ms, "block" | "params"[, fence passed, host submit ms])]
+        (save-back copies; SDMA ones also carry when the device passed the copy's fence, or None,
+        and when the host submitted it)}."""
         if self._trace_ref is None:
             return {"loads": [], "compute": [], "d2h": []}
         self.drain()
@@ -577,14 +588,22 @@ class AsyncTransferEngine:
         ref = self._trace_ref
         compute = [(bid, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev)) for bid, s_ev, e_ev in self._trace_compute]
         d2h, untimed = [], 0
-        for n, s_ev, e_ev, kind in self._trace_d2h:
+        for n, s_ev, e_ev, kind, *when in self._trace_d2h:
             if isinstance(s_ev, SaveBackTicket):  # copy-engine times, aligned at start_trace
                 try:
                     t0, t1 = s_ev.times_ns()
                 except RuntimeError:  # a tool (a profiler's copy tracing) took the copies' signals
                     untimed += 1
                     continue
-                d2h.append((n, (t0 - self._trace_t0_ns) / 1e6, (t1 - self._trace_t0_ns) / 1e6, kind))
+                # then: when the device passed the copy's fence (None when one of its events was
+                # recorded before the trace, untimed), when the host submitted it
+                fence_evs, submitted = when
+                try:
+                    fence_ms = max(ref.elapsed_ms(ev) for ev in fence_evs)
+                except (RuntimeError, ValueError):
+                    fence_ms = None
+                d2h.append((n, (t0 - self._trace_t0_ns) / 1e6, (t1 - self._trace_t0_ns) / 1e6, kind,
+                            fence_ms, (submitted - self._trace_t0_host) * 1e3))
             else:
                 d2h.append((n, ref.elapsed_ms(s_ev), ref.elapsed_ms(e_ev), kind))
         out = {"loads": list(self._trace_loads), "compute": compute, "d2h": d2h, "d2h_untimed": untimed,
@@ -607,14 +626,26 @@ class AsyncTransferEngine:
 
     # ── asynchronous parameter save-back ─────────────────────────────
 
-    def d2h_async(self, tensors: list[torch.Tensor]) -> tuple[list[torch.Tensor], "NativeEvent | SaveBackTicket | None"]:
+    def record_event(self) -> "NativeEvent | None":
+        """An event recorded now on the current stream (None without a GPU): a save-back fence.
+        Timed while a trace runs, so the trace can tell when the device passed it."""
+        if not self._has_cuda:
+            return None
+        ev = NativeEvent(timing=self._trace_ref is not None)
+        ev.record(_current_stream_handle())
+        return ev
+
+    def d2h_async(self, tensors: list[torch.Tensor],
+                  after: "list[NativeEvent] | None" = None) -> tuple[list[torch.Tensor], "NativeEvent | SaveBackTicket | None"]:
         """Copies device tensors into new pinned host tensors (a save-back).
 
         Returns the host tensors and what marks their completion (None without a
         GPU, where the copies are synchronous). The device tensors are kept alive
         until the copies complete (``reap``/``drain``), so the caller may drop its
         references at once. Ordering: the copies start after the work queued so
-        far on the current stream.
+        far on the current stream, or, given ``after``, once the device has passed
+        every one of those events (the caller vouches that no work queued since
+        writes the tensors).
         """
         if not self._has_cuda:
             return [t.detach().to("cpu").clone() for t in tensors], None
@@ -624,22 +655,26 @@ class AsyncTransferEngine:
             if src.device.type == "cpu":
                 outs.append(src.clone())
                 continue
-            src = src.contiguous()
+            if not src.is_contiguous():
+                src = src.contiguous()
+                after = None  # the contiguous copy is queued on the current stream now
             out = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
             outs.append(out)
             pairs.append((out, src))
-        return outs, self._issue_save_back(pairs, "params")
+        return outs, self._issue_save_back(pairs, "params", after)
 
-    def d2h_into(self, src: torch.Tensor, dst: torch.Tensor) -> "NativeEvent | SaveBackTicket | None":
+    def d2h_into(self, src: torch.Tensor, dst: torch.Tensor,
+                 after: "list[NativeEvent] | None" = None) -> "NativeEvent | SaveBackTicket | None":
         """One save-back copy of the contiguous device tensor ``src`` into the pinned host tensor
-        ``dst``, after the work queued so far on the current stream; returns its completion."""
+        ``dst``, after the work queued so far on the current stream (or after the events
+        ``after``, as in ``d2h_async``); returns its completion."""
         nbytes = src.numel() * src.element_size()
         if dst.numel() * dst.element_size() < nbytes or not src.is_contiguous() or not dst.is_contiguous():
             raise ValueError("d2h_into needs contiguous tensors and a destination at least as large as the source")
         if not self._has_cuda:
             dst.view(torch.uint8)[:nbytes].copy_(src.reshape(-1).view(torch.uint8))
             return None
-        return self._issue_save_back([(dst, src)], "block")
+        return self._issue_save_back([(dst, src)], "block", after)
 
     def _saveback_engine(self) -> SaveBackEngine | None:
         """The SDMA save-back engine (created on first use), or None when save-backs use the copy stream."""
@@ -654,12 +689,12 @@ class AsyncTransferEngine:
                 return None
         return self._saveback
 
-    def _issue_save_back(self, pairs: list[tuple[torch.Tensor, torch.Tensor]],
-                         kind: str) -> "NativeEvent | SaveBackTicket":
+    def _issue_save_back(self, pairs: list[tuple[torch.Tensor, torch.Tensor]], kind: str,
+                         after: "list[NativeEvent] | None" = None) -> "NativeEvent | SaveBackTicket":
         """Copies each (pinned host dst, device src) pair after the work queued so far on the current
-        stream: on the SDMA engine when there is one (one ticket), else on the copy stream (one
-        event). Either way, completions are in submission order, and the pending list keeps the
-        tensors alive until theirs."""
+        stream, or after the events ``after``: on the SDMA engine when there is one (one ticket),
+        else on the copy stream (one event). Either way, completions are in submission order, and
+        the pending list keeps the tensors alive until theirs."""
         nbytes = sum(src.numel() * src.element_size() for _dst, src in pairs)
         keep = [t for pair in pairs for t in pair]
         sb = self._saveback_engine()
@@ -668,12 +703,27 @@ class AsyncTransferEngine:
             items = np.zeros(len(pairs), dtype=COPY_ITEM_DTYPE)
             for i, (dst, src) in enumerate(pairs):
                 items[i] = (dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size())
-            done = sb.submit(items, _current_stream_handle())
+            if after:
+                # the engine's worker waits for these events themselves (kept alive with the copy)
+                done = sb.submit_after(items, after)
+                keep.extend(after)
+                fence = list(after)
+            else:
+                fence = None
+                if self._trace_ref is not None:
+                    # a timing event where the save-back's fence is recorded: when the device passes it
+                    fence = [NativeEvent(timing=True)]
+                    fence[0].record(_current_stream_handle())
+                done = sb.submit(items, _current_stream_handle())
             if self._trace_ref is not None:
-                self._trace_d2h.append((nbytes, done, None, kind))
+                self._trace_d2h.append((nbytes, done, None, kind, fence, time.perf_counter()))
         else:
             cs = self._copy_stream.cuda_stream
-            self._fence_copy_stream(cs)
+            if after:
+                for ev in after:
+                    ev.wait_on(cs)
+            else:
+                self._fence_copy_stream(cs)
             t_start = None
             if self._trace_ref is not None:
                 t_start = NativeEvent(timing=True)

@@ -148,12 +148,15 @@ def test_trace_reports_copy_engine_spans():
     for s, h in zip(srcs, homes):
         eng.d2h_into(s, h)
     tr = eng.stop_trace()
-    spans = [(n, t0, t1) for n, t0, t1, kind in tr["d2h"] if kind == "block"]
+    spans = [(n, t0, t1, fence, sub) for n, t0, t1, kind, fence, sub in tr["d2h"] if kind == "block"]
     assert len(spans) == 3
-    for n, t0, t1 in spans:
+    for n, t0, t1, fence, sub in spans:
         assert n == 64 << 20
         assert -1.0 < t0 < t1 < 10_000.0
         assert n / ((t1 - t0) * 1e-3) < 100e9  # no faster than a PCIe link can go
+        # the copy starts after the device passed its fence (the copy engine's clock and the HIP
+        # timeline are aligned to within a millisecond), which it reaches after the host submits
+        assert -1.0 < fence <= t0 + 1.0 and sub >= 0.0
     for s, h in zip(srcs, homes):
         assert torch.equal(h, s.cpu())
     eng.shutdown()
@@ -234,3 +237,34 @@ def test_release_of_earlier_tickets_while_a_later_one_is_waited_for():
     eng.drain()
     eng.shutdown()
     pool.shutdown()
+
+
+def test_submit_after_waits_for_its_events_not_for_the_stream():
+    """``submit_after`` copies once its events have completed, while the stream they were recorded
+    on is still busy; with no events it copies at once. Both complete in submission order."""
+    import time
+
+    from tests.test_streaming_gpu import _sleep_cycles_for
+
+    sb = SaveBackEngine(torch.cuda.current_device())
+    g = torch.Generator(device="cuda").manual_seed(9)
+    srcs = [torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g) for n in (16 << 20, 4097)]
+    dsts = [torch.zeros(s.numel(), dtype=torch.uint8, pin_memory=True) for s in srcs]
+    ready = NativeEvent()
+    ready.record(_stream())  # the sources are final here
+    spin = _sleep_cycles_for(400.0)
+    torch.cuda._sleep(spin)
+    t0 = time.perf_counter()
+    first = sb.submit_after(_items([(dsts[0], srcs[0])]), [ready])
+    second = sb.submit_after(_items([(dsts[1], srcs[1])]), [])
+    second.synchronize()  # covers the first ticket too
+    took = time.perf_counter() - t0
+    assert first.query() and took < 0.2, f"{took * 1e3:.0f} ms"
+    for d, s in zip(dsts, srcs):
+        assert torch.equal(d, s.cpu())
+    with pytest.raises(ValueError, match="event 0 is NULL"):
+        import types
+
+        sb.submit_after(_items([(dsts[1], srcs[1])]), [types.SimpleNamespace(handle=ctypes.c_void_p())])
+    torch.cuda.synchronize()
+    sb.close()

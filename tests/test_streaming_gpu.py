@@ -436,3 +436,71 @@ def test_pinned_pieces_go_straight_to_the_device_after_their_save_back():
     assert pool2.stats()["peak_in_use"] == 0
     eng2.shutdown()
     pool2.shutdown()
+
+
+def _sleep_cycles_for(ms: float) -> int:
+    """Cycles of torch.cuda._sleep (a bounded spin kernel) that keep the current stream busy for
+    about ``ms`` milliseconds on this device."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    probe = 1_000_000
+    torch.cuda._sleep(probe)
+    start.record()
+    torch.cuda._sleep(probe)
+    end.record()
+    end.synchronize()
+    return int(min(probe / max(start.elapsed_time(end), 1e-3) * ms, 4_000_000_000))
+
+
+def test_save_back_fence_is_the_blocks_last_use_unless_a_parameter_changed():
+    """Inside a step, a module-backed block's save-back waits for the block's last hook and the
+    step's start, not for the compute queued after them; a parameter changed in place since the
+    step began makes it wait for everything queued, so the host copy carries the change (the
+    reference copies synchronously at eviction, scheduler.py:1216-1226)."""
+    import time
+
+    model = init_(TinyStack(n=3, hidden=64, mlp=2), seed=11).to(torch.bfloat16)
+    rt = stagehand.StagehandRuntime(model, _config(prefetch_window_blocks=1), block_pattern=r"^blocks\.\d+$",
+                                    dtype=torch.bfloat16, inference_mode=False)
+    sched = rt.scheduler
+    x = torch.randn(4, 64).to(torch.bfloat16).cuda()
+    # a first step evicts blocks 0 and 1 once, so their pinned host buffers exist (allocating
+    # pinned memory may wait for the device)
+    rt.begin_step(0)
+    with torch.no_grad(), rt.managed_forward():
+        model(x)
+    sched._evict_block("blocks.0", save_back=True)
+    sched._evict_block("blocks.1", save_back=True)
+    rt.end_step()
+    rt.begin_step(1)
+    with torch.no_grad(), rt.managed_forward():
+        model(x)
+    torch.cuda.synchronize()
+    names = [n for n, _ in model.blocks[1].named_parameters()]
+    want1 = {n: p.detach().cpu().clone() for n, p in model.blocks[1].named_parameters()}
+    spin = _sleep_cycles_for(400.0)
+
+    # block 1, unchanged: its save-back completes while the compute stream is still spinning
+    torch.cuda._sleep(spin)
+    t0 = time.perf_counter()
+    sched._evict_block("blocks.1", save_back=True, wait=False)
+    t_call = time.perf_counter() - t0
+    fence = sched._d2h_fences["blocks.1"]
+    while not fence.query() and time.perf_counter() - t0 < 5.0:
+        time.sleep(0.001)
+    took = time.perf_counter() - t0
+    assert took < 0.2, f"the save-back completed after {took * 1e3:.0f} ms (the call took {t_call * 1e3:.0f} ms)"
+    for n, p in model.blocks[1].named_parameters():
+        assert p.device.type == "cpu" and torch.equal(_bits(p), _bits(want1[n])), n
+    torch.cuda.synchronize()
+
+    # block 0, changed in place after its last hook, behind a spin: the copy sees the change
+    p0 = dict(model.blocks[0].named_parameters())[names[0]]
+    want0 = (p0.detach().float() + 1.0).to(torch.bfloat16).cpu()
+    torch.cuda._sleep(spin)
+    with torch.no_grad():
+        p0.add_(1.0)
+    sched._evict_block("blocks.0", save_back=True)
+    got = dict(model.blocks[0].named_parameters())[names[0]]
+    assert got.device.type == "cpu" and torch.equal(_bits(got), _bits(want0))
+    rt.end_step()
+    rt.shutdown()
