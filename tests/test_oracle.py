@@ -10,6 +10,7 @@ index, an FMA-style reassociation) fail these pins.
 """
 from __future__ import annotations
 
+import os
 from fractions import Fraction
 from pathlib import Path
 
@@ -74,16 +75,24 @@ def test_bf16_matches_exact_rational_rounding():
 
 
 @pytest.mark.slow
+def _bf16_first_mismatch(start: int, count: int) -> int | None:
+    u = np.arange(start, start + count, dtype=np.uint32)
+    f = u.view(np.float32)
+    want = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    bad = np.flatnonzero(oq.bf16_rne_bits(f) != want)
+    return None if bad.size == 0 else int(u[bad[0]])
+
+
 def test_bf16_exhaustive_against_torch():
-    """All 2^32 fp32 bit patterns: the oracle equals torch's CPU conversion."""
-    chunk = 1 << 26
-    for start in range(0, 1 << 32, chunk):
-        u = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32)
-        f = u.view(np.float32)
-        want = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
-        got = oq.bf16_rne_bits(f)
-        bad = np.flatnonzero(got != want)
-        assert bad.size == 0, f"chunk {start:#x}: first mismatch at {int(u[bad[0]]):#010x}"
+    """All 2^32 fp32 bit patterns: the oracle equals torch's CPU conversion (chunks on threads:
+    numpy and torch release the GIL in these loops)."""
+    import concurrent.futures
+
+    chunk = 1 << 22
+    starts = range(0, 1 << 32, chunk)
+    with concurrent.futures.ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:
+        for start, bad in zip(starts, ex.map(_bf16_first_mismatch, starts, [chunk] * len(starts))):
+            assert bad is None, f"chunk {start:#x}: first mismatch at {bad:#010x}"
 
 
 # ── dequant ────────────────────────────────────────────────────────────────
