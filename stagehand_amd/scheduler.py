@@ -230,6 +230,9 @@ class StagehandScheduler:
         self._step_versions: dict[str, tuple[int, ...]] = {}
         self._in_step = False
         self._grad_hooks: list = []
+        # blocks loaded since their last after_block: the load (and the gradients moved to the
+        # device with it) may still be writing them, so their save-backs wait for the whole queue
+        self._unsettled: set[str] = set()
         # device memory that an eviction gave up is left out of the budget while the
         # save-back copy still holds it (the reference's synchronous copy frees it at once)
         count_as_released = getattr(budget, "count_as_released", None)
@@ -326,10 +329,12 @@ class StagehandScheduler:
         accumulation belongs to other blocks: it reads their parameters, not this block's. The
         optimizer and other work between steps is before the step's start. So the copy needs only
         those events, and the save-back engine need not wait for compute queued far ahead of it
-        (the host runs ahead of the device by up to max_run_ahead_blocks blocks). A parameter
-        changed in place since the step began (its version counter moved) takes the whole queue.
-        Writes through ``param.data`` do not move the counter and are not seen here."""
-        if not self._in_step or module is None:
+        (the host runs ahead of the device by up to max_run_ahead_blocks blocks). The whole queue
+        is waited for when a parameter changed in place since the step began (its version counter
+        moved) and when the block was loaded again after its last hook (the load, and gradients
+        moved to the device with it, write it; the eviction has ordered the current stream after
+        the load). Writes through ``param.data`` do not move the counter and are not seen here."""
+        if not self._in_step or module is None or block_id in self._unsettled:
             return None
         versions = self._step_versions.get(block_id)
         if versions is None or versions != tuple(p._version for p in module.parameters()):
@@ -599,6 +604,8 @@ class StagehandScheduler:
 
     def after_block(self, block_id: str, output: torch.Tensor | None = None) -> None:
         self._engine.mark_compute(block_id, start=False)
+        # the compute stream waited for the block's load before this block ran
+        self._unsettled.discard(block_id)
         if self._in_step and block_id in self._step_versions:
             self._record_last_use(block_id)
         self._mark_block_done()
@@ -684,6 +691,7 @@ class StagehandScheduler:
             else:
                 handle = self._engine.submit_h2d(block_id, staged, res_entry.gpu_tensor)
             self._pending_handles[block_id] = handle
+            self._unsettled.add(block_id)
             self._residency.transition(block_id, BlockState.PREFETCHING)
             self._telemetry.record_h2d(block_entry.size_bytes)
 
@@ -1001,6 +1009,7 @@ class StagehandScheduler:
             source = self._build_module_source(block_entry, module, layout)
             res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True,
                                                             wait_event=d2h_fence, pinned_pieces=True)
+            self._unsettled.add(block_id)
             if d2h_fence is not None and any(p.grad is not None and p.grad.device.type == "cpu"
                                              for p in module.parameters()):
                 # saved-back gradients move to the device on the current stream, after their save-back

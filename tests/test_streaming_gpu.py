@@ -504,3 +504,38 @@ def test_save_back_fence_is_the_blocks_last_use_unless_a_parameter_changed():
     assert got.device.type == "cpu" and torch.equal(_bits(got), _bits(want0))
     rt.end_step()
     rt.shutdown()
+
+
+def test_save_back_of_a_block_evicted_while_its_load_is_in_flight():
+    """A block evicted right after its load was submitted, never used, is copied back with the
+    loaded values: its save-back waits for everything queued, which the eviction ordered after the
+    load, and not only for the step's start. The load reads the block's pinned host buffer, which
+    the save-back then writes, so a save-back that ran first would put the device's stale bytes
+    back into it."""
+    model = init_(TinyStack(n=2, hidden=2048, mlp=4), seed=12).to(torch.bfloat16)
+    cfg = _config(prefetch_window_blocks=1, pinned_pool_mb=512, pinned_slab_mb=64)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                    inference_mode=False)
+    sched = rt.scheduler
+    x = torch.randn(4, 2048).to(torch.bfloat16).cuda()
+    rt.begin_step(0)
+    with torch.no_grad(), rt.managed_forward():
+        model(x)
+    for b in ("blocks.0", "blocks.1"):
+        sched._evict_block(b, save_back=True)
+    rt.end_step()
+    # the host values (views of the block's pinned buffer) change between steps: the device
+    # buffer the next load reuses still holds the old ones
+    with torch.no_grad():
+        for p in model.blocks[0].parameters():
+            p.add_(1.0)
+    want = {n: p.detach().clone() for n, p in model.blocks[0].named_parameters()}
+    rt.begin_step(1)
+    torch.cuda._sleep(_sleep_cycles_for(300.0))
+    for _ in range(3):
+        sched._load_block_to_gpu("blocks.0")
+        sched._evict_block("blocks.0", save_back=True)
+    for n, p in model.blocks[0].named_parameters():
+        assert p.device.type == "cpu" and torch.equal(_bits(p), _bits(want[n])), n
+    rt.end_step()
+    rt.shutdown()
