@@ -300,7 +300,8 @@ class StagehandScheduler:
         their trainable parameters until end_step (for the save-back fences)."""
         self._remove_grad_hooks()
         record = getattr(self._engine, "record_event", None)
-        self._step_mark = record() if self._has_cuda and callable(record) else None
+        # inference evicts without save-backs (the eviction loop), so it needs none of this
+        self._step_mark = record() if self._has_cuda and callable(record) and not self._inference_mode else None
         self._in_step = self._step_mark is not None
         if not self._in_step:
             return
