@@ -235,3 +235,55 @@ def test_direct_eviction_waits_for_its_save_back_but_the_loop_does_not():
     sched._budget.below_low_watermark = MagicMock(side_effect=[False, True])
     sched._run_eviction()
     assert calls == [("evict", "block_1")]
+
+
+def test_save_back_fence_follows_the_last_use_and_the_step_start():
+    """Which events a module-backed block's save-back waits for (host logic; the events are
+    recorded on the device in real runs, stand-ins here): outside a step and in inference, the whole
+    queue (None); inside a step, the step's start and the block's last use (its after_block or a
+    gradient accumulation into it); the whole queue again once a parameter changed in place or the
+    block was loaded after its last hook. The gradient hooks last from begin_step to end_step."""
+    events = []
+
+    def record():
+        events.append(object())
+        return events[-1]
+
+    def begin(sched, step):
+        # begin_step with the device-only bookkeeping switched on
+        sched._has_cuda = True
+        try:
+            sched.begin_step(step)
+        finally:
+            sched._has_cuda = False
+
+    sched, _b, _t, _res, reg, _p, model = _stack(n=3, window=1)
+    sched._engine.record_event = record
+    assert sched._save_back_fence("block_1", model.block_1) is None
+    begin(sched, 0)
+    step_mark = events[-1]
+    assert len(sched._grad_hooks) == 3  # one per trainable parameter of the three blocks
+    assert sched._save_back_fence("block_1", model.block_1) == [step_mark]
+    sched.before_block("block_1")
+    sched.after_block("block_1")
+    assert sched._save_back_fence("block_1", model.block_1) == [events[-1], step_mark]
+    # a gradient accumulated into block 0 marks its last use
+    model.block_0(torch.randn(2, 16, dtype=model.block_0.weight.dtype)).float().sum().backward()
+    assert sched._save_back_fence("block_0", model.block_0) == [events[-1], step_mark]
+    # a block loaded again since its last hook: the whole queue, until its next after_block
+    sched._unsettled.add("block_2")
+    assert sched._save_back_fence("block_2", model.block_2) is None
+    sched.before_block("block_2")
+    sched.after_block("block_2")
+    assert sched._save_back_fence("block_2", model.block_2) == [events[-1], step_mark]
+    # a parameter changed in place since the step began: the whole queue
+    with torch.no_grad():
+        model.block_1.weight.add_(1.0)
+    assert sched._save_back_fence("block_1", model.block_1) is None
+    sched.end_step()
+    assert sched._grad_hooks == [] and sched._save_back_fence("block_2", model.block_2) is None
+
+    inf, *_rest, inf_model = _stack(n=2, window=1, inference=True)
+    inf._engine.record_event = record
+    begin(inf, 0)
+    assert inf._save_back_fence("block_0", inf_model.block_0) is None and inf._grad_hooks == []
