@@ -39,6 +39,28 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def settle_launches(fn, settle_ms: float, stream) -> dict:
+    """Runs fn() back to back for about settle_ms of wall time before a timed leg.
+
+    From an idle GPU the config-2 kernels take 30-50 launches to reach their steady rate: the
+    dequant's per-launch time falls from about 1.14 ms to 1.04 ms over its first 20 launches. The
+    timed launches therefore follow a settle phase of the same kernel. The first 20 settle
+    launches are timed too and reported as the cold-start average, so both figures are visible."""
+    if settle_ms <= 0:
+        return {"settle_ms": 0}
+    _wall, per = time_launches(fn, 20, 0, stream)
+    import torch
+
+    t0 = time.perf_counter()
+    n = 20
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(10):
+            fn()
+        n += 10
+        torch.cuda.synchronize()
+    return {"settle_ms": settle_ms, "settle_launches": n, "cold_first20_ms_avg": round(sum(per) / len(per), 5)}
+
+
 def time_launches(fn, steps: int, warmup: int, stream) -> tuple[float, list[float]]:
     """Runs fn() warmup+steps times; returns (wall ms for the timed steps, per-launch ms)."""
     import torch
@@ -692,10 +714,10 @@ def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | Non
     return out
 
 
-def kernel_stats(trace_dir: Path, skip: int) -> dict:
+def kernel_stats(trace_dir: Path, last: int) -> dict:
     """Per-kernel dispatch statistics of a rocprofv3 ``--kernel-trace`` CSV for the library's kernels
-    (``sh_*``), over the dispatches after the first ``skip`` of each kernel (the bench's warm-up
-    launches), in µs."""
+    (``sh_*``), over the last ``last`` dispatches of each kernel (the bench's timed launches, after
+    its settle and warm-up launches), in µs."""
     import csv
     import statistics
 
@@ -711,7 +733,7 @@ def kernel_stats(trace_dir: Path, skip: int) -> dict:
                                                  (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3))
     out = {}
     for name, rows in sorted(per.items()):
-        d = [us for _t, us in sorted(rows)][skip:]
+        d = [us for _t, us in sorted(rows)][-last:]
         if d:
             out[name] = {"calls": len(d), "avg_us": round(statistics.fmean(d), 2), "min_us": round(min(d), 2),
                          "max_us": round(max(d), 2), "median_us": round(statistics.median(d), 2)}
@@ -1368,6 +1390,9 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--skip-extras", action="store_true", help="omit cast / PCIe / D2D measurements")
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--settle-ms", type=float, default=500.0,
+                    help="config-2 legs: run the kernel this long before the warm-up and timed launches "
+                         "(0 times from an idle GPU)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only launch each kernel a few times (dequant, cast, 1 GiB copy) for counter runs")
     ap.add_argument("--dit", default="both", choices=["none", "squareq", "file", "both"],
@@ -1397,8 +1422,8 @@ def main() -> int:
                     help="only summarise the copy/compute overlap of a rocprofv3 CSV trace in DIR (no GPU)")
     ap.add_argument("--trace-bytes", type=int, default=None, help="H2D bytes inside the marked window")
     ap.add_argument("--kernel-stats", default=None, metavar="DIR",
-                    help="only print per-kernel dispatch statistics of a rocprofv3 kernel trace in DIR (no GPU); "
-                         "the first --warmup dispatches of each kernel are left out")
+                    help="only print per-kernel dispatch statistics of a rocprofv3 kernel trace in DIR (no GPU) "
+                         "over the last --steps dispatches of each kernel")
     ap.add_argument("--pmc-summary", nargs="+", default=None, metavar="DIR",
                     help="only print per-kernel medians of rocprofv3 --pmc CSVs under DIRs (no GPU)")
     ap.add_argument("--pcie-gbps", type=float, default=None, help="measured pinned H2D GB/s for --trace-summary")
@@ -1414,7 +1439,7 @@ def main() -> int:
         print(json.dumps(trace_summary(Path(args.trace_summary), args.trace_bytes, args.pcie_gbps)), flush=True)
         return 0
     if args.kernel_stats:
-        print(json.dumps(kernel_stats(Path(args.kernel_stats), args.warmup), indent=1), flush=True)
+        print(json.dumps(kernel_stats(Path(args.kernel_stats), args.steps), indent=1), flush=True)
         return 0
     if args.pmc_summary:
         print(json.dumps(pmc_summary([Path(d) for d in args.pmc_summary]), indent=1), flush=True)
@@ -1464,7 +1489,8 @@ def main() -> int:
     def step():
         dequant_i8_rowscale_bf16(plan, src, scales, dst, stream=stream)
 
-    log(f"dequant: warmup {args.warmup}, timed {args.steps}")
+    log(f"dequant: settle {args.settle_ms:g} ms, warmup {args.warmup}, timed {args.steps}")
+    settle = settle_launches(step, args.settle_ms, stream)
     wall_ms, per = time_launches(step, args.steps, args.warmup, stream)
     avg_ms = sum(per) / len(per)
     gbps = algo / (avg_ms * 1e-3) / 1e9
@@ -1501,6 +1527,7 @@ def main() -> int:
             "traffic": traffic,
             "kernel_ms_avg": round(avg_ms, 5),
             "kernel_ms_min": round(min(per), 5),
+            **settle,
         },
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
     }
@@ -1520,6 +1547,7 @@ def main() -> int:
         def cstep():
             unpack_cast_f32_bf16(cplan, csrc, dst, stream=stream)
 
+        c_settle = settle_launches(cstep, args.settle_ms, stream)
         c_wall, c_per = time_launches(cstep, args.steps, args.warmup, stream)
         c_avg = sum(c_per) / len(c_per)
         c_gbps = cplan.info["algo_bytes"] / (c_avg * 1e-3) / 1e9
@@ -1530,6 +1558,7 @@ def main() -> int:
             "gbps": round(c_gbps, 2),
             "hbm_frac": round(c_gbps / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic("sh_cast_f32_bf16_kernel"),
+            **c_settle,
         }
         if not args.skip_cpu:
             log("cpu baseline: the reference's host fp32->bf16 pack")
