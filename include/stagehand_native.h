@@ -146,7 +146,8 @@ typedef struct sh_unpack_desc {
   uint64_t div_magic;  /* ceil(2^64 / cols), 0 when cols == 1 */
   uint32_t tile_begin; /* first tile of this descriptor */
   uint32_t ntiles;     /* tiles covering rows*cols elements */
-  uint32_t flags;      /* reserved, 0 */
+  uint32_t lead;       /* elements before element 0 in the first tile, so that the tiles' destination
+                          spans start on 64-byte boundaries (0 when the region start allows none) */
   uint32_t reserved;
 } sh_unpack_desc;     /* 64 bytes, identical layout on host and device */
 

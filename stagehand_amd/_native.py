@@ -80,7 +80,7 @@ DESC_DTYPE = np.dtype(
         ("div_magic", "<u8"),
         ("tile_begin", "<u4"),
         ("ntiles", "<u4"),
-        ("flags", "<u4"),
+        ("lead", "<u4"),
         ("reserved", "<u4"),
     ]
 )

@@ -117,6 +117,36 @@ def test_plan_describe_counts_and_extents():
     assert info["kind_mask"] == 1 << KIND_I8_ROWSCALE_BF16
 
 
+def test_plan_tiles_start_on_destination_lines():
+    """A region whose destination starts inside a 64-byte line gets a lead of elements before its
+    element 0, so every wavefront's destination span starts on a line; the lead is a whole number of
+    chunks (8 int8, 4 fp32, 16 bytes of copy, 32 of zero fill) or nothing."""
+    t_i8 = describe([(KIND_I8_ROWSCALE_BF16, 0, 0, 1, 1 << 16, 0, 0)])["tile_elems"]
+    t_f32 = (1 << 20) // describe([(KIND_F32_BF16, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
+    t_copy = (1 << 20) // describe([(KIND_COPY_BYTES, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
+    t_zero = (1 << 20) // describe([(KIND_ZERO_BYTES, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
+
+    def tiles(kind, dst_off, numel):
+        return describe([(kind, 0, dst_off, 1, numel, 0, 0)])["n_tiles"]
+
+    # exactly one tile of elements: a lead adds a tile, no lead keeps one
+    assert tiles(KIND_I8_ROWSCALE_BF16, 16, t_i8) == 2      # lead 8 elements (16 B)
+    assert tiles(KIND_I8_ROWSCALE_BF16, 48, t_i8) == 2      # lead 24
+    assert tiles(KIND_I8_ROWSCALE_BF16, 64, t_i8) == 1      # on a line already
+    assert tiles(KIND_I8_ROWSCALE_BF16, 18, t_i8) == 1      # 9 elements: not whole chunks
+    assert tiles(KIND_I8_ROWSCALE_BF16, 8, t_i8) == 1       # 4 elements: not whole chunks
+    assert tiles(KIND_F32_BF16, 8, t_f32) == 2              # lead 4
+    assert tiles(KIND_F32_BF16, 4, t_f32) == 1              # 2 elements
+    assert tiles(KIND_COPY_BYTES, 16, t_copy) == 2
+    assert tiles(KIND_COPY_BYTES, 8, t_copy) == 1
+    assert tiles(KIND_ZERO_BYTES, 32, t_zero) == 2
+    assert tiles(KIND_ZERO_BYTES, 16, t_zero) == 1
+    assert tiles(KIND_BF16_F32, 16, 1 << 16) == tiles(KIND_BF16_F32, 0, 1 << 16)  # 16-element chunks: never
+    # the lead is counted in the last tile too: numel + lead elements
+    assert tiles(KIND_I8_ROWSCALE_BF16, 16, t_i8 - 8) == 1
+    assert tiles(KIND_I8_ROWSCALE_BF16, 16, t_i8 - 7) == 2
+
+
 def test_plan_describe_padded_source_extent():
     info = describe([(KIND_I8_ROWSCALE_BF16, 0, 0, 6, 10, 16, 0)])
     assert info["src_extent"] == 5 * 16 + 10

@@ -196,6 +196,59 @@ def test_mixed_plan_all_kinds_match_oracle():
     assert (got[:2] == 0x5A).all() and (got[pos:] == 0x5A).all()
 
 
+@pytest.mark.parametrize("line_off", [8, 16, 24, 32, 48, 56])
+def test_regions_starting_inside_a_destination_line(line_off):
+    """Destinations that start inside a 64-byte line, where the plan places a lead of elements
+    before each region so the tiles' spans start on lines: every kind, regions of several tiles with
+    ragged ends, padded int8 rows, byte canaries between the regions."""
+    rng = np.random.default_rng(line_off)
+    w = rng.integers(-127, 128, (70, 3072), dtype=np.int8)          # several int8 tiles
+    wp = rng.integers(-127, 128, (13, 104), dtype=np.int8)          # padded rows: 96 of 104 used
+    ws = rng.integers(-127, 128, (9, 40), dtype=np.int8)            # fp32 out
+    s = np.exp(rng.normal(-6, 0.5, 70 + 13 + 9)).astype(np.float32)
+    f = rng.normal(0, 1, 5000).astype(np.float32)                   # cast, ragged end
+    bf = oq.cast_f32_bf16(rng.normal(0, 1, 3000).astype(np.float32))
+    raw = rng.integers(0, 256, 9000, dtype=np.uint8)
+    src, (o_w, o_wp, o_ws, o_f, o_bf, o_raw) = _pack([w, wp, ws, f, bf, raw], start=line_off, align=16)
+    sizes = [("w", 70 * 3072 * 2), ("wp", 13 * 96 * 2), ("ws", 9 * 40 * 4), ("f", 5000 * 2), ("bf", 3000 * 4),
+             ("raw", 9000), ("z", 7000)]
+    doff, pos = {}, 0
+    for name, nb in sizes:
+        pos = (pos + 63) // 64 * 64 + line_off    # every region starts line_off bytes into a line
+        doff[name] = pos
+        pos += nb
+    descs = make_descs([
+        (KIND_I8_ROWSCALE_BF16, o_w, doff["w"], 70, 3072, 0, 0),
+        (KIND_I8_ROWSCALE_BF16, o_wp, doff["wp"], 13, 96, 104, 70),
+        (KIND_I8_ROWSCALE_F32, o_ws, doff["ws"], 9, 40, 0, 83),
+        (KIND_F32_BF16, o_f, doff["f"], 1, 5000, 0, 0),
+        (KIND_BF16_F32, o_bf, doff["bf"], 1, 3000, 0, 0),
+        (KIND_COPY_BYTES, o_raw, doff["raw"], 1, 9000, 0, 0),
+        (KIND_ZERO_BYTES, 0, doff["z"], 1, 7000, 0, 0),
+    ])
+    dst = torch.full((pos + 64,), 0x5A, dtype=torch.uint8, device="cuda")
+    UnpackPlan(descs).run(_dev(src), dst, _dev(s))
+    torch.cuda.synchronize()
+    got = dst.cpu().numpy()
+    written = np.zeros(got.size, bool)
+
+    def region(name, nb):
+        written[doff[name]:doff[name] + nb] = True
+        return got[doff[name]:doff[name] + nb]
+
+    np.testing.assert_array_equal(region("w", 70 * 3072 * 2).view(np.uint16),
+                                  oq.dequant_rows(w, s[:70], None, 70, 3072).reshape(-1))
+    np.testing.assert_array_equal(region("wp", 13 * 96 * 2).view(np.uint16),
+                                  oq.dequant_rows(wp, s[70:83], None, 13, 96).reshape(-1))
+    np.testing.assert_array_equal(region("ws", 9 * 40 * 4).view(np.uint32),
+                                  oq.dequant_rows(ws, s[83:], None, 9, 40, out="float32").view(np.uint32).reshape(-1))
+    np.testing.assert_array_equal(region("f", 10000).view(np.uint16), oq.cast_f32_bf16(f))
+    np.testing.assert_array_equal(region("bf", 12000).view(np.float32), oq.bf16_bits_to_f32(bf))
+    np.testing.assert_array_equal(region("raw", 9000), raw)
+    assert not region("z", 7000).any()
+    assert (got[~written] == 0x5A).all(), "wrote outside its regions"
+
+
 def test_cast_golden_vectors_including_nan():
     z = _golden("bf16_cast.npz")
     f = z["f32_bits"].view(np.float32)
