@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 5
+#define SH_ABI_VERSION 6
 
 enum sh_status {
   SH_OK = 0,
@@ -381,6 +381,14 @@ typedef struct sh_load_request {
    * for wait_event). Do not release the ticket before the load completes. */
   struct sh_saveback* saveback;
   uint64_t saveback_ticket;
+  /* Optional digests of the destination once written (no reference counterpart; for
+   * sh_saveback_submit_chunks): sh_block_digest of dst[0, digest_bytes) in chunks of
+   * digest_chunk bytes into `digest` (device memory), on the loader's unpack stream, before
+   * the load counts as done. */
+  uint64_t* digest;
+  uint64_t digest_bytes;
+  uint32_t digest_chunk;
+  uint32_t reserved2;
 } sh_load_request;
 
 typedef struct sh_loader sh_loader;
@@ -448,6 +456,34 @@ int sh_saveback_release(sh_saveback* sb, uint64_t ticket);
 int sh_saveback_set_timing(sh_saveback* sb, int enable);
 int sh_saveback_clock_ns(uint64_t* ns);
 int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64_t* out2);
+/* Save-back of the chunks that changed (no reference counterpart: the reference copies the
+ * whole block back, src/stagehand/scheduler.py:1216-1226). Copies dev_src[0, bytes) into
+ * host_dst (pinned) in chunks of chunk_bytes, after the caller's events (or, with
+ * n_events == 0, after the work queued on `stream` now), and only the chunks whose digest
+ * differs from `digests` (two uint64 per chunk, as sh_block_digest wrote them, device
+ * memory): once the events have completed, the engine's worker runs sh_block_changed on
+ * `digest_stream` into `changed` (pinned host memory, one byte per chunk), waits for it, and
+ * issues one copy per run of changed chunks. digests == NULL copies every chunk. The caller
+ * vouches that host_dst held the bytes the digests describe. All buffers stay in use until
+ * the ticket completes; sh_saveback_ticket_bytes then gives the bytes copied. */
+int sh_saveback_submit_chunks(sh_saveback* sb, void* host_dst, const void* dev_src, uint64_t bytes,
+                              uint32_t chunk_bytes, const uint64_t* digests, uint8_t* changed, void* digest_stream,
+                              void* const* events, uint32_t n_events, void* stream, uint64_t* ticket);
+/* Waits for the ticket and gives the bytes its copies moved. */
+int sh_saveback_ticket_bytes(sh_saveback* sb, uint64_t ticket, uint64_t* bytes);
+
+/* ───────────────────────── chunk digests ─────────────────────────
+ * Per-chunk digests of a buffer (no reference counterpart), for sh_saveback_submit_chunks
+ * and the load request's `digest`: two uint64 per chunk of chunk_bytes (a positive multiple
+ * of 16; the last chunk may be shorter), the sums over the chunk's 8-byte words of two
+ * bijective 64-bit mixes keyed by the word's position. A change of one word always changes a
+ * chunk's digest. sh_block_digest writes digests[2c], digests[2c + 1] on `stream`;
+ * sh_block_changed writes changed[c] = 1 where the chunk's digest differs from those, else 0;
+ * sh_block_digest_host computes the same digests on the host. */
+int sh_block_digest(const void* buf, uint64_t bytes, uint32_t chunk_bytes, uint64_t* digests, void* stream);
+int sh_block_changed(const void* buf, uint64_t bytes, uint32_t chunk_bytes, const uint64_t* digests, uint8_t* changed,
+                     void* stream);
+int sh_block_digest_host(const void* buf, uint64_t bytes, uint32_t chunk_bytes, uint64_t* digests);
 
 /* ───────────────────────── turbo window engine ─────────────────────────
  * A fixed window of device slots that blocks rotate through: the HIP rewrite

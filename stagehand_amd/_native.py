@@ -175,6 +175,12 @@ _SIGNATURES: dict[str, list] = {
     "sh_saveback_set_timing": [_vp, _i32],
     "sh_saveback_clock_ns": [ctypes.POINTER(ctypes.c_uint64)],
     "sh_saveback_ticket_times": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_submit_chunks": [_vp, _vp, _vp, ctypes.c_uint64, _u32, _vp, _vp, _vp, _vp, _u32, _vp,
+                                  ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_ticket_bytes": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+    "sh_block_digest": [_vp, ctypes.c_uint64, _u32, _vp, _vp],
+    "sh_block_changed": [_vp, ctypes.c_uint64, _u32, _vp, _vp, _vp],
+    "sh_block_digest_host": [_vp, ctypes.c_uint64, _u32, _vp],
     "sh_turbo_create": [ctypes.POINTER(_vp)],
     "sh_turbo_destroy": [_vp],
     "sh_turbo_register_block": [_vp, _vp, _u32, ctypes.POINTER(_u32)],
@@ -224,7 +230,8 @@ LOAD_REQUEST_DTYPE = np.dtype([
     ("staging_bytes", "<u8"), ("dst", "<u8"), ("dst_bytes", "<u8"), ("scale_off", "<i8"), ("zp_off", "<i8"),
     ("n_scale", "<u8"), ("copy_threads", "<i4"), ("reserved", "<i4"), ("image", "<u8"),
     ("ranges", "<u8"), ("n_ranges", "<u8"), ("dma", "<u8"), ("n_dma", "<u8"), ("wait_event", "<u8"),
-    ("saveback", "<u8"), ("saveback_ticket", "<u8"),
+    ("saveback", "<u8"), ("saveback_ticket", "<u8"), ("digest", "<u8"), ("digest_bytes", "<u8"),
+    ("digest_chunk", "<u4"), ("reserved2", "<u4"),
 ])
 
 # Mirrors of `struct sh_file_range` / `struct sh_file_info`.
@@ -251,7 +258,7 @@ TURBO_SPAN_DTYPE = np.dtype([("block", "<u4"), ("kind", "<u4"), ("start_ns", "<u
                              ("bytes", "<u8")])
 TURBO_SPAN_WRITEBACK, TURBO_SPAN_HOST_WAIT = 0, 1
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

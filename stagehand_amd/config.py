@@ -59,6 +59,16 @@ class StagehandConfig:
     #            then run many times slower (measured on a 17.8B-parameter
     #            LoRA training step: 1.75 s per step against 1.13 s with "sdma").
     save_back_engine: str = "sdma"
+    # a module-backed block whose last load came from its pinned home buffer (the
+    # buffer its last whole-block save-back wrote) gets a digest per chunk of
+    # save_back_chunk_bytes on the device after the load; its next save-back
+    # compares the digests and copies back only the chunks that changed (frozen
+    # weights are not copied again). The home buffer ends up holding the device's
+    # bytes, as after the reference's full copy-back (scheduler.py:1216-1226); a
+    # changed chunk goes unnoticed only if both 64-bit sums of its digest collide
+    # (about 2^-128; one changed word is always seen). Needs the "sdma" engine.
+    save_back_changed_chunks: bool = True
+    save_back_chunk_bytes: int = 1 << 20
     # the host waits in before_block until the compute of the block this many
     # blocks back has finished on the device (0: never). Loads and waits are
     # device-side, so without a bound the host can queue work for many blocks

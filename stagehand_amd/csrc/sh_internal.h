@@ -72,6 +72,12 @@ int run_io(const std::vector<IoPiece>& pieces, int threads);
 // the descriptor on which read-ahead advice is worth giving.
 int advice_fd(const sh_file* f);
 
+// Chunk digests (sh_digest.hip): the launches behind sh_block_digest / sh_block_changed, for
+// the loader and the save-back engine.
+int launch_block_digest(const void* buf, uint64_t bytes, uint32_t chunk_bytes, uint64_t* digests, hipStream_t stream);
+int launch_block_changed(const void* buf, uint64_t bytes, uint32_t chunk_bytes, const uint64_t* digests,
+                         uint8_t* changed, hipStream_t stream);
+
 // floor(n / d) for every 32-bit n, with magic = ceil(2^64 / d) for d >= 2 and
 // magic = 0 for d == 1. The quotient is floor(n * magic / 2^64): with
 // magic = 2^64/d + eps (0 <= eps < 1), the error term n*eps/2^64 < 2^-32 <= 1/d

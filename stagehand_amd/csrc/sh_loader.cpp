@@ -79,6 +79,9 @@ struct Ticket {
   uint64_t n_scale = 0;
   int copy_threads = 1;
   void* image = nullptr;
+  uint64_t* digest = nullptr;  // chunk digests of dst once written (sh_block_digest)
+  uint64_t digest_bytes = 0;
+  uint32_t digest_chunk = 0;
 };
 
 }  // namespace
@@ -295,20 +298,29 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   e = hipEventRecord(t.copied, L->copy_stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord(copied)");
   int st = SH_OK;
-  if (t.plan == nullptr) {
+  if (t.plan == nullptr && t.digest == nullptr) {
     e = hipEventRecord(t.done, L->copy_stream);
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
     return SH_OK;
   }
   e = hipStreamWaitEvent(L->unpack_stream, t.copied, 0);
   if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(copied)");
-  const uint8_t* stg = (const uint8_t*)t.staging;
-  const float* scales = t.scale_off >= 0 ? (const float*)(stg + t.scale_off) : nullptr;
-  const float* zps = t.zp_off >= 0 ? (const float*)(stg + t.zp_off) : nullptr;
-  st = sh_unpack(t.plan, t.staging, t.staging_bytes, scales, zps, t.n_scale, t.dst, t.dst_bytes, L->unpack_stream);
-  if (st != SH_OK) {
-    err = sh_last_error();
-    return st;
+  if (t.plan != nullptr) {
+    const uint8_t* stg = (const uint8_t*)t.staging;
+    const float* scales = t.scale_off >= 0 ? (const float*)(stg + t.scale_off) : nullptr;
+    const float* zps = t.zp_off >= 0 ? (const float*)(stg + t.zp_off) : nullptr;
+    st = sh_unpack(t.plan, t.staging, t.staging_bytes, scales, zps, t.n_scale, t.dst, t.dst_bytes, L->unpack_stream);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      return st;
+    }
+  }
+  if (t.digest != nullptr) {
+    st = sh::launch_block_digest(t.dst, t.digest_bytes, t.digest_chunk, t.digest, L->unpack_stream);
+    if (st != SH_OK) {
+      err = sh_last_error();
+      return st;
+    }
   }
   e = hipEventRecord(t.done, L->unpack_stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
@@ -350,10 +362,12 @@ void worker_loop(sh_loader* L) {
     std::string err;
     const int st = run_request(L, *t, err);
     if (st != SH_OK) {
-      // Chunks copied before the failure may still be landing in the destination:
-      // mark their end so that releasing the ticket waits for them.
+      // Chunks copied before the failure may still be landing in the destination, and kernels
+      // queued on the unpack stream may still read it: mark the end of both so that releasing
+      // the ticket waits for them.
       (void)hipEventRecord(t->copied, L->copy_stream);
-      (void)hipEventRecord(t->done, L->copy_stream);
+      (void)hipStreamWaitEvent(L->unpack_stream, t->copied, 0);
+      (void)hipEventRecord(t->done, L->unpack_stream);
     }
     {
       std::lock_guard<std::mutex> lk(L->mu);
@@ -524,6 +538,14 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   } else if (req->dst_bytes < req->src_bytes) {
     return sh::fail(SH_ERR_INVALID, "sh_loader_submit: destination smaller than the source bytes");
   }
+  if (req->digest != nullptr) {
+    if (req->digest_bytes > req->dst_bytes)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: digest of %llu bytes past the destination's %llu",
+                      (unsigned long long)req->digest_bytes, (unsigned long long)req->dst_bytes);
+    if (req->digest_chunk == 0 || req->digest_chunk % 16 != 0)
+      return sh::fail(SH_ERR_INVALID, "sh_loader_submit: digest_chunk %u is not a positive multiple of 16",
+                      req->digest_chunk);
+  }
 
   std::lock_guard<std::mutex> lk(L->mu);
   const uint64_t id = L->next_ticket++;
@@ -555,6 +577,9 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   t.n_scale = req->n_scale;
   t.copy_threads = req->copy_threads > 0 ? req->copy_threads : L->copy_threads;
   t.image = req->image;
+  t.digest = req->digest;
+  t.digest_bytes = req->digest_bytes;
+  t.digest_chunk = req->digest_chunk;
   L->queue.push_back(id);
   *ticket = id;
   L->cv.notify_one();

@@ -56,6 +56,18 @@ struct Job {
   std::vector<hsa_signal_t> done;  // done[k]: 1 until items[k] has been copied
   int status = SH_OK;  // set (under the engine lock) before a failure completes the signals
   std::string error;
+  uint64_t copied = 0;  // bytes the items move
+  // sh_saveback_submit_chunks: the worker picks the copies (items, done, copied) once the
+  // fences have passed, then sets `issued`; until then waiters wait for it.
+  bool chunked = false;
+  uint8_t* host_dst = nullptr;
+  const uint8_t* dev_src = nullptr;
+  uint64_t bytes = 0;
+  uint32_t chunk = 0;
+  const uint64_t* digests = nullptr;
+  uint8_t* changed = nullptr;
+  hipStream_t digest_stream = nullptr;
+  bool issued = true;  // guarded by the engine lock
 
   Job() = default;
   Job(const Job&) = delete;
@@ -89,6 +101,8 @@ struct sh_saveback {
   uint64_t next_id = 1;
   bool stop = false;
   std::atomic<bool> timing{false};  // read by the worker without the lock
+  std::condition_variable issued_cv;  // a chunk job's copies were picked
+  hipEvent_t compared = nullptr;      // the worker's: end of a chunk job's digest comparison
   std::thread worker;
 };
 
@@ -101,8 +115,62 @@ void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, size
     std::lock_guard<std::mutex> lk(sb->mu);
     j.status = status;
     j.error = what;
+    j.issued = true;  // a chunk job that failed before its copies were picked has none
   }
+  sb->issued_cv.notify_all();
   for (size_t k = first; k < j.done.size(); ++k) hsa_signal_subtract_screlease(j.done[k], 1);
+}
+
+// For a chunk job whose fences have passed: compares the chunks' digests (when given), then
+// sets the job's copies, one per run of changed chunks, with a signal each, and publishes them.
+int pick_chunks(sh_saveback* sb, Job& j, std::string& err) {
+  const uint64_t n = (j.bytes + j.chunk - 1) / j.chunk;
+  if (j.digests != nullptr) {
+    int st = sh::launch_block_changed(j.dev_src, j.bytes, j.chunk, j.digests, j.changed, j.digest_stream);
+    if (st != SH_OK) {
+      err = std::string("sh_block_changed: ") + sh_last_error();
+      return st;
+    }
+    hipError_t e = hipEventRecord(sb->compared, j.digest_stream);
+    if (e == hipSuccess) e = hipEventSynchronize(sb->compared);
+    if (e != hipSuccess) {
+      err = std::string("digest comparison: ") + hipGetErrorString(e);
+      return SH_ERR_HIP;
+    }
+  }
+  std::vector<sh_copy_item> runs;
+  const volatile uint8_t* changed = j.changed;
+  for (uint64_t c = 0; c < n;) {
+    if (j.digests != nullptr && changed[c] == 0) {
+      ++c;
+      continue;
+    }
+    uint64_t c1 = c + 1;
+    while (c1 < n && (j.digests == nullptr || changed[c1] != 0)) ++c1;
+    const uint64_t b = c * j.chunk, e = std::min<uint64_t>(c1 * j.chunk, j.bytes);
+    runs.push_back(sh_copy_item{j.host_dst + b, j.dev_src + b, e - b});
+    c = c1;
+  }
+  std::vector<hsa_signal_t> sigs;
+  for (size_t k = 0; k < runs.size(); ++k) {
+    hsa_signal_t s{0};
+    if (hsa_signal_create(1, 0, nullptr, &s) != HSA_STATUS_SUCCESS) {
+      for (hsa_signal_t t : sigs) hsa_signal_destroy(t);
+      err = "hsa_signal_create failed";
+      return SH_ERR_HIP;
+    }
+    sigs.push_back(s);
+  }
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    j.copied = 0;
+    for (const sh_copy_item& r : runs) j.copied += r.bytes;
+    j.items = std::move(runs);
+    j.done = std::move(sigs);
+    j.issued = true;
+  }
+  sb->issued_cv.notify_all();
+  return SH_OK;
 }
 
 void worker_loop(sh_saveback* sb) {
@@ -123,6 +191,14 @@ void worker_loop(sh_saveback* sb) {
       fail_job(sb, *j, SH_ERR_HIP, std::string("hipEventSynchronize(save-back fence): ") + hipGetErrorString(e), 0);
       continue;
     }
+    if (j->chunked) {
+      std::string err;
+      const int st = pick_chunks(sb, *j, err);
+      if (st != SH_OK) {
+        fail_job(sb, *j, st, err, 0);
+        continue;
+      }
+    }
     for (size_t k = 0; k < j->items.size(); ++k) {
       const sh_copy_item& it = j->items[k];
       hsa_status_t s = hsa_amd_memory_async_copy(it.dst, sb->cpu, it.src, sb->gpu, it.bytes, 0, nullptr, j->done[k]);
@@ -139,6 +215,10 @@ void worker_loop(sh_saveback* sb) {
 
 // Waits for `j` alone; SH_OK or its failure (recorded in the last error).
 int wait_job(sh_saveback* sb, const std::shared_ptr<Job>& j) {
+  {
+    std::unique_lock<std::mutex> lk(sb->mu);
+    sb->issued_cv.wait(lk, [&] { return j->issued; });  // a chunk job's copies are picked by the worker
+  }
   bool negative = false;
   for (hsa_signal_t s : j->done) {
     hsa_signal_value_t v;
@@ -152,7 +232,11 @@ int wait_job(sh_saveback* sb, const std::shared_ptr<Job>& j) {
   return SH_OK;
 }
 
-bool job_done(const Job& j) {
+bool job_done(sh_saveback* sb, const Job& j) {
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    if (!j.issued) return false;
+  }
   for (hsa_signal_t s : j.done)
     if (hsa_signal_load_scacquire(s) >= 1) return false;
   return true;
@@ -201,6 +285,11 @@ extern "C" int sh_saveback_create(int device, sh_saveback** out) {
     hsa_shut_down();
     return sh::fail(SH_ERR_HIP, "sh_saveback_create: no CPU agent");
   }
+  e = hipEventCreateWithFlags(&sb->compared, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    hsa_shut_down();
+    return sh::fail(SH_ERR_HIP, "sh_saveback_create: hipEventCreate: %s", hipGetErrorString(e));
+  }
   sh_saveback* raw = sb.release();
   raw->worker = std::thread(worker_loop, raw);
   *out = raw;
@@ -222,12 +311,16 @@ extern "C" int sh_saveback_destroy(sh_saveback* sb) {
     if (first == SH_OK) first = st;
   }
   sb->jobs.clear();  // the last references: each job's signal and fence go with it
+  if (sb->compared != nullptr) (void)hipEventDestroy(sb->compared);
   delete sb;
   hsa_shut_down();
   return first;
 }
 
 namespace {
+
+int enqueue_job(sh_saveback* sb, const std::shared_ptr<Job>& j, void* stream, void* const* events,
+                uint32_t n_events, uint64_t* ticket);
 
 // Queues a ticket whose copies wait for an event recorded now on `stream` (events == nullptr) or
 // for the caller's events.
@@ -248,9 +341,17 @@ int submit_job(sh_saveback* sb, const sh_copy_item* items, uint64_t n, void* str
       return sh::fail(SH_ERR_HIP, "sh_saveback_submit: hsa_signal_create failed");
     j->done.push_back(s);
   }
+  for (const sh_copy_item& it : j->items) j->copied += it.bytes;
+  return enqueue_job(sb, j, stream, events, n_events, ticket);
+}
+
+// Gives the job its fence (an event recorded now on `stream`, or the caller's events), then
+// queues it for the worker and returns its ticket.
+int enqueue_job(sh_saveback* sb, const std::shared_ptr<Job>& j, void* stream, void* const* events,
+                uint32_t n_events, uint64_t* ticket) {
   // A ticket without copies is complete at once (it has no signals): it gets no fence and
   // never reaches the worker, which only waits for fences and issues copies.
-  const bool empty = j->items.empty();
+  const bool empty = j->items.empty() && !j->chunked;
   if (!empty && events != nullptr) {
     j->after.assign(reinterpret_cast<const hipEvent_t*>(events), reinterpret_cast<const hipEvent_t*>(events) + n_events);
   } else if (!empty) {
@@ -292,6 +393,55 @@ extern "C" int sh_saveback_submit_after(sh_saveback* sb, const sh_copy_item* ite
   return submit_job(sb, items, n, nullptr, n_events ? events : kNone, n_events, ticket);
 }
 
+extern "C" int sh_saveback_submit_chunks(sh_saveback* sb, void* host_dst, const void* dev_src, uint64_t bytes,
+                                         uint32_t chunk_bytes, const uint64_t* digests, uint8_t* changed,
+                                         void* digest_stream, void* const* events, uint32_t n_events, void* stream,
+                                         uint64_t* ticket) {
+  static const char* who = "sh_saveback_submit_chunks";
+  sh::clear_error();
+  if (sb == nullptr || ticket == nullptr || (n_events > 0 && events == nullptr))
+    return sh::fail(SH_ERR_INVALID, "%s: NULL argument", who);
+  *ticket = 0;
+  if (bytes > 0 && (host_dst == nullptr || dev_src == nullptr)) return sh::fail(SH_ERR_INVALID, "%s: NULL buffer", who);
+  if (chunk_bytes == 0 || chunk_bytes % 16 != 0)
+    return sh::fail(SH_ERR_INVALID, "%s: chunk_bytes %u is not a positive multiple of 16", who, chunk_bytes);
+  if (digests != nullptr && changed == nullptr) return sh::fail(SH_ERR_INVALID, "%s: digests without `changed`", who);
+  if ((bytes + chunk_bytes - 1) / chunk_bytes > 0x7FFFFFFFull)
+    return sh::fail(SH_ERR_INVALID, "%s: too many chunks of %u bytes", who, chunk_bytes);
+  for (uint32_t k = 0; k < n_events; ++k)
+    if (events[k] == nullptr) return sh::fail(SH_ERR_INVALID, "%s: event %u is NULL", who, k);
+  auto j = std::make_shared<Job>();
+  if (bytes > 0) {
+    j->chunked = true;
+    j->issued = false;
+    j->host_dst = (uint8_t*)host_dst;
+    j->dev_src = (const uint8_t*)dev_src;
+    j->bytes = bytes;
+    j->chunk = chunk_bytes;
+    j->digests = digests;
+    j->changed = changed;
+    j->digest_stream = (hipStream_t)digest_stream;
+  }
+  return enqueue_job(sb, j, stream, n_events ? events : nullptr, n_events, ticket);
+}
+
+extern "C" int sh_saveback_ticket_bytes(sh_saveback* sb, uint64_t ticket, uint64_t* bytes) {
+  sh::clear_error();
+  if (sb == nullptr || bytes == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_ticket_bytes: NULL argument");
+  std::shared_ptr<Job> j;
+  {
+    std::lock_guard<std::mutex> lk(sb->mu);
+    auto it = sb->jobs.find(ticket);
+    if (it == sb->jobs.end()) return sh::fail(SH_ERR_INVALID, "sh_saveback_ticket_bytes: unknown or released ticket");
+    j = it->second;
+  }
+  int st = wait_job(sb, j);
+  if (st != SH_OK) return st;
+  std::lock_guard<std::mutex> lk(sb->mu);
+  *bytes = j->copied;
+  return SH_OK;
+}
+
 extern "C" int sh_saveback_query(sh_saveback* sb, uint64_t ticket) {
   sh::clear_error();
   if (sb == nullptr) return sh::fail(SH_ERR_INVALID, "sh_saveback_query: NULL engine");
@@ -299,7 +449,7 @@ extern "C" int sh_saveback_query(sh_saveback* sb, uint64_t ticket) {
   int st = jobs_upto(sb, ticket, js, "sh_saveback_query");
   if (st != SH_OK) return st;
   for (const auto& j : js) {
-    if (!job_done(*j)) return SH_ERR_NOT_READY;
+    if (!job_done(sb, *j)) return SH_ERR_NOT_READY;
     st = wait_job(sb, j);  // every signal at its final value: returns at once
     if (st != SH_OK) return st;
   }

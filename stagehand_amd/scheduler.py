@@ -220,6 +220,12 @@ class StagehandScheduler:
         self._host_copies: dict[str, dict[str, torch.Tensor]] = {}
         # block → pinned host buffer in the block's layout, the target of its whole-block save-backs
         self._host_homes: dict[str, torch.Tensor] = {}
+        # save-backs of changed chunks (config.save_back_changed_chunks): per block, the device
+        # buffer of its chunk digests, the (digests, bytes) its last load from the home buffer
+        # wrote, and the pinned byte-per-chunk flags its save-backs compare into
+        self._digest_bufs: dict[str, torch.Tensor] = {}
+        self._load_digests: dict[str, tuple[torch.Tensor, int]] = {}
+        self._changed_flags: dict[str, torch.Tensor] = {}
         # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
         self._done_marks: collections.deque = collections.deque()
         # save-back fences (_save_back_fence): per module-backed block, an event after its last
@@ -416,14 +422,62 @@ class StagehandScheduler:
                 return False
             end = max(end, off + numel * dtype.itemsize)
         home = self._host_homes.get(block_id)
-        if home is None or home.numel() < end:
+        fresh = home is None or home.numel() < end
+        if fresh:
             home = torch.empty(end, dtype=torch.uint8, pin_memory=True)
             self._host_homes[block_id] = home
-        ev = self._engine.d2h_into(base[:end], home[:end], after=self._save_back_fence(block_id, module))
+        after = self._save_back_fence(block_id, module)
+        loaded = self._load_digests.pop(block_id, None)
+        ev = None
+        if not fresh and loaded is not None and loaded[1] == end:
+            # the block was loaded from this home buffer and its digests taken then: copy back the
+            # chunks that changed on the device since
+            chunk = self._chunk_bytes()
+            n_chunks = -(-end // chunk)
+            flags = self._changed_flags.get(block_id)
+            if flags is None or flags.numel() < n_chunks:
+                flags = torch.zeros(n_chunks, dtype=torch.uint8, pin_memory=True)
+                self._changed_flags[block_id] = flags
+            ev = self._engine.d2h_changed(base[:end], home[:end], chunk, loaded[0], flags, after=after)
+        if ev is None:
+            ev = self._engine.d2h_into(base[:end], home[:end], after=after)
         _restore_params_from_tensor(module, home, layout)
         if ev is not None:
             self._d2h_fences[block_id] = ev
         return True
+
+    def _chunk_bytes(self) -> int:
+        return int(getattr(self._config, "save_back_chunk_bytes", 1 << 20))
+
+    def _home_load_digest(self, block_id: str, module: nn.Module, layout) -> tuple[torch.Tensor, int] | None:
+        """Where a module-backed load writes its chunk digests, or None for no digests.
+
+        Digests are taken only when the load's source is exactly the block's home buffer (every
+        parameter its view at its layout offset, in the layout's dtype, as a whole-block
+        save-back left them): the device then starts out with the home buffer's bytes, so its
+        next save-back may skip the chunks whose digests have not changed. A source built any
+        other way (parameters replaced on the host, a cast on load) takes a full save-back."""
+        if not (self._has_cuda and getattr(self._config, "save_back_changed_chunks", False)
+                and getattr(self._config, "save_back_engine", "sdma") == "sdma"):
+            return None
+        home = self._host_homes.get(block_id)
+        if home is None or layout is None:
+            return None
+        hptr, end = home.data_ptr(), 0
+        for name, _shape, dtype, off, numel in layout:
+            d = _get_param_data(module, name)
+            if (d.device.type != "cpu" or d.dtype != dtype or d.numel() != numel or not d.is_contiguous()
+                    or d.data_ptr() != hptr + off):
+                return None
+            end = max(end, off + numel * dtype.itemsize)
+        if end == 0 or end > home.numel():
+            return None
+        n_words = 2 * -(-end // self._chunk_bytes())
+        dig = self._digest_bufs.get(block_id)
+        if dig is None or dig.numel() < n_words:
+            dig = torch.empty(n_words, dtype=torch.int64, device="cuda")  # two uint64 sums per chunk
+            self._digest_bufs[block_id] = dig
+        return dig, end
 
     def _release_with_save_back(self, block_id: str, res_entry: ResidencyEntry, fence_before: Any) -> None:
         """The block's device buffer, about to be dropped, stays held by the whole-block save-back
@@ -529,6 +583,9 @@ class StagehandScheduler:
         self._file_maps.clear()
         self._weight_files.close()
         self._host_homes.clear()
+        self._digest_bufs.clear()
+        self._load_digests.clear()
+        self._changed_flags.clear()
         self._v2_locations.clear()
         self._squareq_layers.clear()
         self._module_param_caches.clear()
@@ -1008,8 +1065,14 @@ class StagehandScheduler:
         gpu_bytes = gpu_tensor.view(torch.uint8)
         if self._has_cuda:
             source = self._build_module_source(block_entry, module, layout)
-            res_entry.load = self._engine.submit_block_load(block_id, source, gpu_bytes, dest_on_loader_stream=True,
-                                                            wait_event=d2h_fence, pinned_pieces=True)
+            digest = self._home_load_digest(block_id, module, layout)
+            res_entry.load = self._engine.submit_block_load(
+                block_id, source, gpu_bytes, dest_on_loader_stream=True, wait_event=d2h_fence, pinned_pieces=True,
+                digest=None if digest is None else (digest[0], digest[1], self._chunk_bytes()))
+            if digest is None:
+                self._load_digests.pop(block_id, None)
+            else:
+                self._load_digests[block_id] = digest
             self._unsettled.add(block_id)
             if d2h_fence is not None and any(p.grad is not None and p.grad.device.type == "cpu"
                                              for p in module.parameters()):

@@ -129,6 +129,20 @@ class SaveBackEngine:
                      handles, len(events), ctypes.byref(ticket))
         return SaveBackTicket(self, ticket.value)
 
+    def submit_chunks(self, host_dst: int, dev_src: int, nbytes: int, chunk: int, digests: int, changed: int,
+                      digest_stream: int, events: "list[NativeEvent] | None", stream_handle: int) -> "SaveBackTicket":
+        """Copies the chunks of ``dev_src`` whose digest differs from ``digests`` (device pointer;
+        0 copies every chunk) into ``host_dst``, after ``events`` (or after the work queued so far
+        on ``stream_handle``): the worker compares them on ``digest_stream`` into ``changed``
+        (pinned, one byte per chunk). Every buffer stays in use until the ticket completes."""
+        ticket = ctypes.c_uint64()
+        evs = events or []
+        handles = (ctypes.c_void_p * max(1, len(evs)))(*[ev.handle.value for ev in evs])
+        _native.call("sh_saveback_submit_chunks", self.handle, host_dst, dev_src, nbytes, chunk, digests or None,
+                     changed or None, digest_stream, handles if evs else None, len(evs), stream_handle,
+                     ctypes.byref(ticket))
+        return SaveBackTicket(self, ticket.value, counts_bytes=True)
+
     def set_timing(self, enable: bool) -> None:
         _native.call("sh_saveback_set_timing", self.handle, int(enable))
         self._timing = bool(enable)
@@ -157,9 +171,11 @@ class SaveBackTicket:
     ``wait_on`` waits on the host, and a load that reads what it wrote passes it as
     ``submit_block_load(wait_event=...)``, which the loader's worker waits for."""
 
-    def __init__(self, engine: SaveBackEngine, ticket: int) -> None:
+    def __init__(self, engine: SaveBackEngine, ticket: int, counts_bytes: bool = False) -> None:
         self.engine = engine
         self.ticket = ticket
+        # a chunk save-back: its copies (and so its bytes) are known once it completes
+        self.counts_bytes = counts_bytes
 
     def query(self) -> bool:
         if self.engine.closed:  # closing the engine waited for every copy
@@ -173,6 +189,12 @@ class SaveBackTicket:
     def wait_on(self, stream_handle: int) -> None:
         """Waits on the host (the copy engine's completion has no device-side wait)."""
         self.synchronize()
+
+    def copied_bytes(self) -> int:
+        """Waits for the ticket; the bytes its copies moved."""
+        out = ctypes.c_uint64()
+        _native.call("sh_saveback_ticket_bytes", self.engine.handle, self.ticket, ctypes.byref(out))
+        return out.value
 
     def times_ns(self) -> tuple[int, int]:
         out = (ctypes.c_uint64 * 2)()
@@ -259,6 +281,8 @@ class AsyncTransferEngine:
         # int8 source, not its bf16 size; telemetry keeps the reference's block sizes)
         self.bytes_h2d = 0
         self.bytes_d2h = 0
+        # bytes handed to chunk save-backs (d2h_changed), before leaving out the unchanged chunks
+        self.bytes_d2h_requested = 0
         self.loads = 0
         # save-back copies in flight: (completion event, device/host tensors they read or
         # write, device bytes their caller gave up with them)
@@ -312,6 +336,10 @@ class AsyncTransferEngine:
         cs, us = ctypes.c_void_p(), ctypes.c_void_p()
         _native.call("sh_loader_streams", self._loader_handle(), ctypes.byref(cs), ctypes.byref(us))
         return cs.value, us.value
+
+    def _loader_unpack_stream(self) -> int:
+        """The loader's unpack stream (hipStream_t value): where chunk digests are taken."""
+        return self.loader_streams()[1]
 
     def _loader_copy_stream(self) -> torch.cuda.ExternalStream:
         if self._loader_stream is None:
@@ -381,7 +409,8 @@ class AsyncTransferEngine:
 
     def submit_block_load(self, block_id: str, source: BlockSource, gpu_dest: torch.Tensor,
                           dest_on_loader_stream: bool = False, wait_event: "NativeEvent | SaveBackTicket | None" = None,
-                          pinned_pieces: bool = False) -> TransferHandle:
+                          pinned_pieces: bool = False,
+                          digest: "tuple[torch.Tensor, int, int] | None" = None) -> TransferHandle:
         """Stage ``source`` into a pinned slab and land it in ``gpu_dest`` (device path).
 
         The copy waits for the work queued on the current stream (``gpu_dest`` may reuse
@@ -393,7 +422,9 @@ class AsyncTransferEngine:
         callers whose pieces are never pinned leave it off);
         ``wait_event`` (such as the save-back copy that wrote them) orders every copy after it: on
         the device for a :class:`NativeEvent`, on the loader's worker thread for a
-        :class:`SaveBackTicket`."""
+        :class:`SaveBackTicket`. ``digest`` = (device tensor of 2 uint64 per chunk, bytes, chunk
+        bytes): the chunk digests of ``gpu_dest``'s first bytes are written there once the load
+        has landed, before it counts as done (for :meth:`d2h_changed`)."""
         if not self._has_cuda:
             raise RuntimeError("submit_block_load needs a GPU")
         dst_bytes = gpu_dest.numel() * gpu_dest.element_size()
@@ -464,6 +495,14 @@ class AsyncTransferEngine:
             req[0]["saveback_ticket"] = wait_event.ticket
         elif wait_event is not None:
             req[0]["wait_event"] = wait_event.handle.value
+        if digest is not None:
+            dig, nbytes, chunk = digest
+            if nbytes > dst_bytes or dig.numel() * dig.element_size() < 16 * (-(-nbytes // chunk)):
+                raise ValueError(f"block {block_id}: digest buffer too small for {nbytes} bytes in chunks of {chunk}")
+            req[0]["digest"] = dig.data_ptr()
+            req[0]["digest_bytes"] = nbytes
+            req[0]["digest_chunk"] = chunk
+            keep.append(dig)
         if source.plan is not None:
             if dest_on_loader_stream:
                 with torch.cuda.stream(self._loader_copy_stream()):
@@ -590,6 +629,10 @@ class AsyncTransferEngine:
         d2h, untimed = [], 0
         for n, s_ev, e_ev, kind, *when in self._trace_d2h:
             if isinstance(s_ev, SaveBackTicket):  # copy-engine times, aligned at start_trace
+                if n is None:  # a chunk save-back: the bytes of its changed chunks
+                    n = s_ev.copied_bytes()
+                    if n == 0:
+                        continue
                 try:
                     t0, t1 = s_ev.times_ns()
                 except RuntimeError:  # a tool (a profiler's copy tracing) took the copies' signals
@@ -675,6 +718,37 @@ class AsyncTransferEngine:
             dst.view(torch.uint8)[:nbytes].copy_(src.reshape(-1).view(torch.uint8))
             return None
         return self._issue_save_back([(dst, src)], "block", after)
+
+    def d2h_changed(self, src: torch.Tensor, dst: torch.Tensor, chunk: int, digests: torch.Tensor,
+                    changed: torch.Tensor, after: "list[NativeEvent] | None" = None) -> "SaveBackTicket | None":
+        """Save-back of the chunks of ``src`` (contiguous, on the device) whose digests differ from
+        ``digests`` (written by a load's ``digest``) into ``dst`` (pinned host, which holds the bytes
+        those digests describe), ordered as ``d2h_into``; ``changed`` is a pinned uint8 tensor of
+        one byte per chunk. Returns None when this engine has no SDMA save-back engine (the caller
+        then copies the whole tensor)."""
+        sb = self._saveback_engine() if self._has_cuda else None
+        if sb is None:
+            return None
+        nbytes = src.numel() * src.element_size()
+        n_chunks = -(-nbytes // chunk)
+        if (dst.numel() * dst.element_size() < nbytes or not src.is_contiguous() or not dst.is_contiguous()
+                or changed.numel() < n_chunks or digests.numel() * digests.element_size() < 16 * n_chunks):
+            raise ValueError("d2h_changed: buffers do not match the chunks")
+        done = sb.submit_chunks(dst.data_ptr(), src.data_ptr(), nbytes, chunk, digests.data_ptr(), changed.data_ptr(),
+                                self._loader_unpack_stream(), after, _current_stream_handle())
+        keep = [dst, src, digests, changed]
+        if after:
+            keep.extend(after)
+        if self._trace_ref is not None:
+            fence = list(after) if after else None
+            if fence is None:
+                fence = [NativeEvent(timing=True)]
+                fence[0].record(_current_stream_handle())
+            self._trace_d2h.append((None, done, None, "block", fence, time.perf_counter()))
+        self.bytes_d2h_requested += nbytes
+        with self._lock:
+            self._pending_d2h.append((done, keep, 0))
+        return done
 
     def _saveback_engine(self) -> SaveBackEngine | None:
         """The SDMA save-back engine (created on first use), or None when save-backs use the copy stream."""
@@ -794,6 +868,10 @@ class AsyncTransferEngine:
             with self._lock:
                 if self._pending_d2h and self._pending_d2h[0][0] is ev:
                     self._releasing_bytes -= self._pending_d2h.pop(0)[2]
+                else:
+                    continue
+            if getattr(ev, "counts_bytes", False):
+                self.bytes_d2h += ev.copied_bytes()  # complete: returns at once
 
     # ── completion ───────────────────────────────────────────────────
 

@@ -268,3 +268,67 @@ def test_submit_after_waits_for_its_events_not_for_the_stream():
         sb.submit_after(_items([(dsts[1], srcs[1])]), [types.SimpleNamespace(handle=ctypes.c_void_p())])
     torch.cuda.synchronize()
     sb.close()
+
+
+@pytest.mark.parametrize("n,chunk", [((6 << 20) + 7, 1 << 20), (3 * 4096, 4096), (4096 * 40 + 16, 4096)])
+def test_submit_chunks_copies_the_changed_chunks(n, chunk):
+    """The chunk form of a save-back: the host buffer holds what the digests describe, the device
+    buffer then changes in some chunks (the first, the last partial one, two adjacent ones, one
+    alone); after the ticket the host buffer equals the device buffer, only the changed chunks were
+    copied (adjacent ones as one run), and with no change nothing is copied."""
+    lib = _native.lib()
+    g = torch.Generator(device="cuda").manual_seed(n)
+    dev = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g)
+    n_chunks = -(-n // chunk)
+    host = torch.empty(n + 64, dtype=torch.uint8, pin_memory=True)
+    host[:n].copy_(dev.cpu())
+    host[n:] = 0xEE
+    dig = torch.zeros(2 * n_chunks, dtype=torch.int64, device="cuda")
+    assert lib.sh_block_digest(dev.data_ptr(), n, chunk, dig.data_ptr(), _stream()) == _native.SH_OK
+    flags = torch.zeros(n_chunks, dtype=torch.uint8, pin_memory=True)
+    eng = AsyncTransferEngine(PinnedPool(total_mb=4, slab_mb=1, alignment=512), save_back="sdma")
+    sb = eng._saveback_engine()
+    unpack = eng._loader_unpack_stream()
+
+    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None,
+                         _stream())
+    assert t.copied_bytes() == 0
+    hit = sorted({0, n_chunks - 1, 1, 2, n_chunks // 2 + 1} & set(range(n_chunks)))
+    for c in hit:
+        dev[min(c * chunk + 3, n - 1)] += 1
+    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None,
+                         _stream())
+    copied = t.copied_bytes()
+    assert copied == sum(min(chunk, n - c * chunk) for c in hit)
+    assert torch.equal(host[:n], dev.cpu()) and (host[n:] == 0xEE).all()
+    np.testing.assert_array_equal(np.flatnonzero(flags.numpy()), hit)
+    # without digests: every chunk, in one run
+    dev.add_(3)
+    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, 0, 0, unpack, None, _stream())
+    assert t.copied_bytes() == n and torch.equal(host[:n], dev.cpu())
+    eng.shutdown()
+
+
+def test_d2h_changed_waits_for_its_events_and_counts_copied_bytes():
+    """``AsyncTransferEngine.d2h_changed`` after caller events: the comparison runs once the events
+    have passed (a write queued before them is seen), and ``bytes_d2h`` counts the copied chunks
+    when the ticket is reaped."""
+    chunk = 1 << 20
+    n = 8 * chunk
+    eng = AsyncTransferEngine(PinnedPool(total_mb=4, slab_mb=1, alignment=512), save_back="sdma")
+    dev = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+    host = dev.cpu().pin_memory()
+    dig = torch.zeros(16, dtype=torch.int64, device="cuda")
+    assert _native.lib().sh_block_digest(dev.data_ptr(), n, chunk, dig.data_ptr(), _stream()) == _native.SH_OK
+    flags = torch.zeros(8, dtype=torch.uint8, pin_memory=True)
+    torch.cuda._sleep(50_000_000)
+    dev[5 * chunk + 17] += 1  # queued behind the spin
+    ev = eng.record_event()
+    before = eng.bytes_d2h
+    t = eng.d2h_changed(dev, host, chunk, dig, flags, after=[ev])
+    t.synchronize()
+    eng.reap()
+    assert torch.equal(host, dev.cpu())
+    assert np.flatnonzero(flags.numpy()).tolist() == [5]
+    assert eng.bytes_d2h - before == chunk and eng.bytes_d2h_requested == n
+    eng.shutdown()

@@ -293,14 +293,15 @@ def _train_dit(seed: int):
     return init_train_dit_(TrainDiT(depth=4, hidden=128, heads=4, mlp_ratio=2.0, rank=8), seed)
 
 
-@pytest.mark.parametrize("frozen_host_copies,save_back", [(False, "sdma"), (True, "sdma"), (False, "stream")])
-def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back):
+@pytest.mark.parametrize("frozen_host_copies,save_back,changed_chunks",
+                         [(False, "sdma", False), (False, "sdma", True), (True, "sdma", False), (False, "stream", False)])
+def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back, changed_chunks):
     """Config-5 shape in small: frozen base weights, trainable LoRA, activation checkpointing
     (blocks recomputed in backward under the runtime's hooks), module-backed eviction every
     block, an SGD step on the LoRA parameters between steps. Outputs, LoRA gradients and the
     updated LoRA weights match the same model trained unstreamed; with frozen host copies the
-    frozen weights are not copied back at eviction. Save-backs on the SDMA engine and on the copy
-    stream."""
+    frozen weights are not copied back at eviction; with changed-chunk save-backs only the first
+    save-back of a block copies all of it. Save-backs on the SDMA engine and on the copy stream."""
     from bench_workloads import TRAIN_BLOCK_PATTERN
 
     model = _train_dit(5)
@@ -312,7 +313,8 @@ def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back):
     target = torch.randn(1, 32, 128, generator=g).cuda()
     base_mb = torch.cuda.memory_allocated() / 2**20
     cfg = _config(vram_high_watermark_mb=int(base_mb) + 1, vram_low_watermark_mb=int(base_mb), prefetch_window_blocks=1,
-                  frozen_host_copies=frozen_host_copies, save_back_engine=save_back)
+                  frozen_host_copies=frozen_host_copies, save_back_engine=save_back,
+                  save_back_changed_chunks=changed_chunks, save_back_chunk_bytes=4096)
     rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
                                     inference_mode=False)
     lora = [p for n, p in model.named_parameters() if "lora" in n]
@@ -350,6 +352,9 @@ def test_checkpointed_lora_training_round_trip(frozen_host_copies, save_back):
     assert evictions > 0
     if frozen_host_copies:
         assert sent_back <= evictions * 2 * lora_per_block
+    elif changed_chunks:
+        assert rt.engine.bytes_d2h_requested > 0
+        assert sent_back < evictions * frozen_per_block
     else:
         assert sent_back >= evictions * frozen_per_block
     rt.shutdown()
@@ -537,5 +542,80 @@ def test_save_back_of_a_block_evicted_while_its_load_is_in_flight():
         sched._evict_block("blocks.0", save_back=True)
     for n, p in model.blocks[0].named_parameters():
         assert p.device.type == "cpu" and torch.equal(_bits(p), _bits(want[n])), n
+    rt.end_step()
+    rt.shutdown()
+
+
+def test_changed_chunk_save_back_round_trip():
+    """Save-backs of the chunks a block changed on the device: the first save-back of a block copies
+    it whole into its pinned home buffer; a load from that buffer takes chunk digests; the next
+    save-back copies exactly the chunks written since (an in-place change at the first and at the
+    last parameter), and one with no change copies nothing. The host values always equal what the
+    device held, as after the reference's full copy-back (scheduler.py:1216-1226); a change made to
+    the host values between steps travels to the device and is kept."""
+    chunk = 4096
+    model = init_(TinyStack(n=2, hidden=256, mlp=2), seed=21).to(torch.bfloat16)
+    cfg = _config(prefetch_window_blocks=1, save_back_chunk_bytes=chunk)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                    inference_mode=False)
+    sched, eng = rt.scheduler, rt.engine
+    block = model.blocks[0]
+    x = torch.randn(4, 256).to(torch.bfloat16).cuda()
+
+    def sent(fn):
+        torch.cuda.synchronize()
+        before = eng.bytes_d2h
+        fn()
+        sched._sync_d2h_fences()
+        eng.reap()
+        return eng.bytes_d2h - before
+
+    rt.begin_step(0)
+    with torch.no_grad(), rt.managed_forward():
+        model(x)
+    first = sent(lambda: sched._evict_block("blocks.0", save_back=True))
+    rt.end_step()
+    size = sum(p.numel() * 2 for p in block.parameters())
+    assert first == size  # no home buffer yet: the whole block
+    layout = None
+    for step in (1, 2):
+        rt.begin_step(step)
+        sched._load_block_to_gpu("blocks.0")
+        sched._await_pending_load("blocks.0")  # the current stream waits for the load on the device
+        assert "blocks.0" in sched._load_digests
+        layout = sched._residency.get_entry("blocks.0").param_layout
+        params = list(block.parameters())
+        with torch.no_grad():
+            params[0].view(-1)[0] += 1
+            params[-1].view(-1)[-1] += 1
+        want = [p.detach().cpu().clone() for p in block.parameters()]
+        got = sent(lambda: sched._evict_block("blocks.0", save_back=True))
+        _name, _shape, dtype, off_last, numel_last = layout[-1]
+        dirty = {0, (off_last + (numel_last - 1) * dtype.itemsize) // chunk}
+        assert got == sum(min(chunk, size - c * chunk) for c in dirty), (step, got)
+        for p, w in zip(block.parameters(), want):
+            assert p.device.type == "cpu" and torch.equal(_bits(p), _bits(w))
+        rt.end_step()
+    # unchanged on the device: nothing copied back
+    rt.begin_step(3)
+    sched._load_block_to_gpu("blocks.0")
+    want = [p.detach().cpu().clone() for p in block.parameters()]
+    assert sent(lambda: sched._evict_block("blocks.0", save_back=True)) == 0
+    for p, w in zip(block.parameters(), want):
+        assert torch.equal(_bits(p), _bits(w))
+    rt.end_step()
+    # changed on the host while evicted: the load carries it, the digests describe it
+    with torch.no_grad():
+        for p in block.parameters():
+            p.add_(1.0)
+    want = [p.detach().clone() for p in block.parameters()]
+    rt.begin_step(4)
+    sched._load_block_to_gpu("blocks.0")
+    sched._await_pending_load("blocks.0")
+    dev = [p.detach().cpu() for p in block.parameters()]
+    assert all(torch.equal(_bits(a), _bits(b)) for a, b in zip(dev, want))
+    assert sent(lambda: sched._evict_block("blocks.0", save_back=True)) == 0
+    for p, w in zip(block.parameters(), want):
+        assert torch.equal(_bits(p), _bits(w))
     rt.end_step()
     rt.shutdown()
