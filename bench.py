@@ -871,7 +871,11 @@ def train_leg(args) -> dict:
                        "bf16 block weights, LoRA r32 on self-attention q/k/v/o = 50.3 M trainable), batch 1 x 4096 "
                        "tokens + 512 conditioning tokens, MSE loss, SGD on LoRA, activation checkpointing, "
                        "VRAM budget 24 GB (watermarks 19200 / 14400 MB), prefetch window 3"}
-    modes = (("reference_eviction", False), ("frozen_host_copies", True))
+    # (label, frozen_host_copies, save_back_changed_chunks): the reference's eviction copies every
+    # parameter back; by default only the chunks changed since the load cross PCIe (the host values
+    # end up the same), and the second mode is the reference's full copy-back
+    modes = (("reference_eviction", False, True), ("reference_eviction_full_copy_back", False, False),
+             ("frozen_host_copies", True, True))
     if args.train_modes == "reference":
         modes = modes[:1]
     if args.release_accounting == "off":
@@ -880,7 +884,7 @@ def train_leg(args) -> dict:
         from stagehand_amd.budget import BudgetManager
 
         BudgetManager.count_as_released = lambda self, releasing_bytes: None
-    for label, fhc in modes:
+    for label, fhc, changed in modes:
         t0 = time.perf_counter()
         with torch.device("meta"):
             model = TrainDiT()
@@ -890,6 +894,7 @@ def train_leg(args) -> dict:
                                         vram_low_watermark_mb=14400, prefetch_window_blocks=3, max_inflight_transfers=4,
                                         nan_inf_check=False, strict_bf16=False, telemetry_enabled=True,
                                         frozen_host_copies=fhc, save_back_engine=args.save_back,
+                                        save_back_changed_chunks=changed,
                                         **({} if args.run_ahead is None else {"max_run_ahead_blocks": args.run_ahead}))
         cfg.telemetry_file = None
         rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
@@ -1406,7 +1411,8 @@ def main() -> int:
     ap.add_argument("--turbo", default="on", choices=["on", "off"], help="config-3 DiT through the turbo window engine")
     ap.add_argument("--train", default="on", choices=["on", "off"], help="config-5 streamed training step")
     ap.add_argument("--train-modes", default="both", choices=["both", "reference"],
-                    help="config 5 with the reference's eviction and with frozen host copies, or the first only")
+                    help="config 5 with the reference's eviction (changed chunks copied back, then every byte) "
+                         "and with frozen host copies, or the first only")
     ap.add_argument("--save-back", default="sdma", choices=["sdma", "stream"],
                     help="where config 5's save-back copies run (StagehandConfig.save_back_engine)")
     ap.add_argument("--vmm", default="on", choices=["on", "off"], help="config-3 DiT served from the VMM backend")
@@ -1680,7 +1686,9 @@ def summary_line(r: dict) -> str:
     if tr:
         for mode, d in tr.items():
             if isinstance(d, dict) and "ms_per_step" in d:
-                parts.append(f"train/{mode} {d['ms_per_step']} ms/step")
+                d2h = d.get("d2h_bytes_per_step")
+                parts.append(f"train/{mode} {d['ms_per_step']} ms/step"
+                             + (f", D2H {d2h / 1e9:.2f} GB/step" if isinstance(d2h, (int, float)) else ""))
     return "summary: " + " | ".join(parts)
 
 

@@ -23,6 +23,12 @@
 // submission order: query and wait report a ticket done only when every live
 // earlier ticket is, so a later ticket covers earlier copies as a later event on
 // one stream would.
+//
+// Chunk save-backs (sh_saveback_submit_chunks): when the caller has digests of what
+// the host buffer holds (sh_digest.hip), the worker, once the fences have passed,
+// compares them with the device buffer on a stream the caller names, waits for that,
+// and copies back only the runs of chunks whose digests changed. Such a ticket's
+// copies are decided by the worker: waiters wait until it has set them.
 
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
