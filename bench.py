@@ -175,6 +175,35 @@ def copy_kernel_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
     return reps * 2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9
 
 
+def digest_kernel_gbps(nbytes: int = 740 << 20, chunk: int = 1 << 20, reps: int = 20) -> dict:
+    """Read rate of the chunk-digest kernel (sh_block_digest; the save-back comparison reads the
+    same bytes) on a buffer the size of a config-5 block, timed on its stream."""
+    import torch
+
+    from stagehand_amd import _native
+
+    a = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    dig = torch.empty(2 * -(-nbytes // chunk), dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    lib = _native.lib()
+
+    def run():
+        _native.check(lib.sh_block_digest(a.data_ptr(), nbytes, chunk, dig.data_ptr(), stream.cuda_stream),
+                      "sh_block_digest")
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(reps):
+        run()
+    e.record(stream)
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    return {"bytes": nbytes, "chunk": chunk, "ms": round(ms, 4), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def host_cores() -> dict:
     """The host cores this process can use: the CPUs it may run on (its affinity set), bounded by
     the cgroup's CPU quota when one is set; ``os.cpu_count()`` (every CPU of the machine) is
@@ -1574,6 +1603,7 @@ def main() -> int:
         log("d2d copy and pinned H2D")
         result["d2d_copy_gbps"] = round(d2d_copy_gbps(), 2)
         result["copy_kernel_gbps"] = round(copy_kernel_gbps(), 2)
+        result["digest_kernel"] = digest_kernel_gbps()
         result["pcie"] = {"h2d_pinned_gbps": round(pinned_h2d_gbps(), 2),
                           "d2h_pinned_gbps": round(pinned_h2d_gbps(d2h=True), 2),
                           "duplex": duplex_gbps(), "transfer_bytes": 1 << 30, "reps": 10}
