@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kDigestThreads) void digest_kernel(const uint8_t* _
                                                                 uint8_t* __restrict__ changed) {
   const uint64_t c = blockIdx.x;
   const uint64_t b = c * chunk;
-  const uint64_t e = (b + chunk < bytes) ? b + chunk : bytes;
+  const uint64_t e = (bytes - b > chunk) ? b + chunk : bytes;
   const uint64_t n16 = (e - b) / 16;
   uint64_t sa = 0, sb = 0;
 #pragma unroll 4
@@ -115,11 +115,15 @@ __global__ __launch_bounds__(kDigestThreads) void digest_kernel(const uint8_t* _
   }
 }
 
+uint64_t chunks_of(uint64_t bytes, uint32_t chunk_bytes) {
+  return bytes / chunk_bytes + (bytes % chunk_bytes != 0 ? 1 : 0);
+}
+
 int check_args(const void* buf, uint64_t bytes, uint32_t chunk_bytes, const void* digests, const char* who) {
   if (chunk_bytes == 0 || chunk_bytes % 16 != 0)
     return sh::fail(SH_ERR_INVALID, "%s: chunk_bytes %u is not a positive multiple of 16", who, chunk_bytes);
   if (bytes > 0 && (buf == nullptr || digests == nullptr)) return sh::fail(SH_ERR_INVALID, "%s: NULL buffer", who);
-  if ((bytes + chunk_bytes - 1) / chunk_bytes > kMaxChunks)
+  if (chunks_of(bytes, chunk_bytes) > kMaxChunks)
     return sh::fail(SH_ERR_INVALID, "%s: %llu bytes make more than %llu chunks of %u bytes", who,
                     (unsigned long long)bytes, (unsigned long long)kMaxChunks, chunk_bytes);
   return SH_OK;
@@ -135,7 +139,7 @@ int launch_block_changed(const void* buf, uint64_t bytes, uint32_t chunk_bytes, 
   if (int st = check_args(buf, bytes, chunk_bytes, digests, "sh_block_changed")) return st;
   if (bytes > 0 && changed == nullptr) return sh::fail(SH_ERR_INVALID, "sh_block_changed: changed is NULL");
   if (bytes == 0) return SH_OK;
-  const uint64_t n = (bytes + chunk_bytes - 1) / chunk_bytes;
+  const uint64_t n = chunks_of(bytes, chunk_bytes);
   hipLaunchKernelGGL(digest_kernel<true>, dim3((uint32_t)n), dim3(kDigestThreads), 0, stream, (const uint8_t*)buf,
                      bytes, (uint64_t)chunk_bytes, const_cast<uint64_t*>(digests), changed);
   SH_HIP(hipGetLastError());
@@ -146,7 +150,7 @@ int launch_block_digest(const void* buf, uint64_t bytes, uint32_t chunk_bytes, u
                         hipStream_t stream) {
   if (int st = check_args(buf, bytes, chunk_bytes, digests, "sh_block_digest")) return st;
   if (bytes == 0) return SH_OK;
-  const uint64_t n = (bytes + chunk_bytes - 1) / chunk_bytes;
+  const uint64_t n = chunks_of(bytes, chunk_bytes);
   hipLaunchKernelGGL(digest_kernel<false>, dim3((uint32_t)n), dim3(kDigestThreads), 0, stream, (const uint8_t*)buf,
                      bytes, (uint64_t)chunk_bytes, digests, (uint8_t*)nullptr);
   SH_HIP(hipGetLastError());
@@ -171,10 +175,10 @@ extern "C" int sh_block_digest_host(const void* buf, uint64_t bytes, uint32_t ch
   sh::clear_error();
   if (int st = check_args(buf, bytes, chunk_bytes, digests, "sh_block_digest_host")) return st;
   const uint8_t* p = (const uint8_t*)buf;
-  const uint64_t n = (bytes + chunk_bytes - 1) / chunk_bytes;
+  const uint64_t n = chunks_of(bytes, chunk_bytes);
   for (uint64_t c = 0; c < n; ++c) {
     const uint64_t b = c * chunk_bytes;
-    const uint64_t e = (b + chunk_bytes < bytes) ? b + chunk_bytes : bytes;
+    const uint64_t e = (bytes - b > chunk_bytes) ? b + chunk_bytes : bytes;
     uint64_t sa = 0, sb = 0, off = b;
     for (; off + 16 <= e; off += 16) {
       uint64_t w[2];

@@ -130,7 +130,7 @@ void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, size
 // For a chunk job whose fences have passed: compares the chunks' digests (when given), then
 // sets the job's copies, one per run of changed chunks, with a signal each, and publishes them.
 int pick_chunks(sh_saveback* sb, Job& j, std::string& err) {
-  const uint64_t n = (j.bytes + j.chunk - 1) / j.chunk;
+  const uint64_t n = j.bytes / j.chunk + (j.bytes % j.chunk != 0 ? 1 : 0);
   if (j.digests != nullptr) {
     int st = sh::launch_block_changed(j.dev_src, j.bytes, j.chunk, j.digests, j.changed, j.digest_stream);
     if (st != SH_OK) {
@@ -153,7 +153,7 @@ int pick_chunks(sh_saveback* sb, Job& j, std::string& err) {
     }
     uint64_t c1 = c + 1;
     while (c1 < n && (j.digests == nullptr || changed[c1] != 0)) ++c1;
-    const uint64_t b = c * j.chunk, e = std::min<uint64_t>(c1 * j.chunk, j.bytes);
+    const uint64_t b = c * j.chunk, e = c1 < n ? c1 * j.chunk : j.bytes;
     runs.push_back(sh_copy_item{j.host_dst + b, j.dev_src + b, e - b});
     c = c1;
   }
@@ -412,7 +412,7 @@ extern "C" int sh_saveback_submit_chunks(sh_saveback* sb, void* host_dst, const 
   if (chunk_bytes == 0 || chunk_bytes % 16 != 0)
     return sh::fail(SH_ERR_INVALID, "%s: chunk_bytes %u is not a positive multiple of 16", who, chunk_bytes);
   if (digests != nullptr && changed == nullptr) return sh::fail(SH_ERR_INVALID, "%s: digests without `changed`", who);
-  if ((bytes + chunk_bytes - 1) / chunk_bytes > 0x7FFFFFFFull)
+  if (bytes / chunk_bytes + (bytes % chunk_bytes != 0 ? 1 : 0) > 0x7FFFFFFFull)
     return sh::fail(SH_ERR_INVALID, "%s: too many chunks of %u bytes", who, chunk_bytes);
   for (uint32_t k = 0; k < n_events; ++k)
     if (events[k] == nullptr) return sh::fail(SH_ERR_INVALID, "%s: event %u is NULL", who, k);
