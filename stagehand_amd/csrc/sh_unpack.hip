@@ -51,9 +51,11 @@ namespace {
 // chunk or two per thread and many short-lived 512-thread workgroups stream
 // best (dequant two chunks of 8 int8 → 16 B of bf16 each per thread; cast one
 // chunk of 4 fp32 → 8 B per thread). Persistent grids, deeper per-thread
-// unrolling, wider chunks and non-temporal loads/stores each measured 5-25%
-// slower, and so did giving each XCD a contiguous run of tiles (dequant 2%,
-// cast 6%): neighbouring tiles on different XCDs stream faster.
+// unrolling and wider chunks each measured 5-25% slower, and so did giving each
+// XCD a contiguous run of tiles (dequant 2%, cast 6%): neighbouring tiles on
+// different XCDs stream faster. Non-temporal accesses help on one side only:
+// the dequant's bf16 stores (+1-1.6%) and the cast's fp32 loads (+1.9%); the
+// other side, or both, measured slower.
 #ifndef SH_UNPACK_THREADS
 #define SH_UNPACK_THREADS 512
 #endif
@@ -130,6 +132,46 @@ __device__ __forceinline__ void stw(uint8_t* p, const Words<NB>& v) {
   __builtin_memcpy(p, &v, NB);
 }
 
+// Non-temporal forms (the `nt` bit on the load / store): 8 or 16 bytes, any byte alignment.
+typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32x4_a1 __attribute__((ext_vector_type(4), aligned(1)));
+
+template <uint32_t NB>
+__device__ __forceinline__ Words<NB> ldw_nt(const uint8_t* p) {
+  static_assert(NB == 8 || NB == 16, "8- or 16-byte non-temporal loads");
+  Words<NB> v;
+  if constexpr (NB == 8) {
+    const u32x2_a1 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_a1*>(p));
+    v.w[0] = x.x;
+    v.w[1] = x.y;
+  } else {
+    const u32x4_a1 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a1*>(p));
+    v.w[0] = x.x;
+    v.w[1] = x.y;
+    v.w[2] = x.z;
+    v.w[3] = x.w;
+  }
+  return v;
+}
+
+template <uint32_t NB>
+__device__ __forceinline__ void stw_nt(uint8_t* p, const Words<NB>& v) {
+  static_assert(NB == 8 || NB == 16, "8- or 16-byte non-temporal stores");
+  if constexpr (NB == 8) {
+    u32x2_a1 x;
+    x.x = v.w[0];
+    x.y = v.w[1];
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x2_a1*>(p));
+  } else {
+    u32x4_a1 x;
+    x.x = v.w[0];
+    x.y = v.w[1];
+    x.z = v.w[2];
+    x.w = v.w[3];
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4_a1*>(p));
+  }
+}
+
 // Rounded bf16 in bits 31..16 (low half is garbage): u + 0x7FFF + lsb.
 __device__ __forceinline__ uint32_t rne_hi(float x) {
   const uint32_t u = __float_as_uint(x);
@@ -174,7 +216,7 @@ __device__ __forceinline__ void dq_chunk_store(const Words<C>& q, float s, float
       o.w[2 * w] = NANCHK ? pack_hi(rne_hi_nan(f0), rne_hi_nan(f1)) : pack_hi(rne_hi(f0), rne_hi(f1));
       o.w[2 * w + 1] = NANCHK ? pack_hi(rne_hi_nan(f2), rne_hi_nan(f3)) : pack_hi(rne_hi(f2), rne_hi(f3));
     }
-    stw<2 * C>(out, o);
+    stw_nt<2 * C>(out, o);  // written once, read by the next kernel: no reason to keep it in L2
   } else {
     Words<4 * C> o;
 #pragma unroll
@@ -310,7 +352,7 @@ __device__ __forceinline__ void tile_f32_bf16(const sh_unpack_desc& d, uint32_t 
 #pragma unroll
   for (uint32_t k = 0; k < U; ++k) {
     const uint32_t e = e0 + k * (kThreads * C);
-    if (e < numel && numel - e >= C) v[k] = ldw<4 * C>(s + (size_t)e * 4);
+    if (e < numel && numel - e >= C) v[k] = ldw_nt<4 * C>(s + (size_t)e * 4);  // read once
   }
 #pragma unroll
   for (uint32_t k = 0; k < U; ++k) {
