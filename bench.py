@@ -813,9 +813,10 @@ def _dit_host_bf16(seed: int):
 def turbo_leg(args) -> dict:
     """The config-3 DiT (bf16, 23.7 GB of blocks) through the turbo window engine:
     every block pinned on the host, a window of 3 device slots, one H2D per block
-    per step. Run twice: the engine's own layout (contiguous slots, no write-back
-    of frozen blocks) and the reference's layout (a slot tensor per parameter,
-    write-back of every evicted block)."""
+    per step. Run in the engine's own layout (contiguous slots, no write-back of
+    frozen blocks) and in the reference's layout (a slot tensor per parameter,
+    write-back of every evicted block), its write-backs of changed chunks and of
+    every byte."""
     import gc
 
     import torch
@@ -826,12 +827,16 @@ def turbo_leg(args) -> dict:
     img, txt, vec = _dit_inputs(args.seed)
     out = {"workload": "config3 bf16 Flux-style DiT (19 double + 38 single blocks, 11.84 B params), module-backed "
                        "weights pinned on the host, turbo window of 3 slots, 4096 image + 512 text tokens, inference"}
-    for label, contiguous, wb in (("engine_layout", True, "auto"), ("reference_layout", False, "always")):
+    # the reference layout writes every evicted block back (engine.rs:232-262): by default only the
+    # chunks changed on the device cross PCIe (the host regions end up the same); then every byte
+    legs = (("engine_layout", True, "auto", 1 << 20), ("reference_layout", False, "always", 1 << 20),
+            ("reference_layout_full_write_back", False, "always", 0))
+    for label, contiguous, wb, chunk in legs:
         t0 = time.perf_counter()
         model = _dit_host_bf16(args.seed)
         flops = dit_forward_flops(model, 4096, 512)
         cond = TurboConductor(model, block_pattern=DIT_BLOCK_PATTERN, dtype=torch.bfloat16,
-                              contiguous_slots=contiguous, writeback=wb)
+                              contiguous_slots=contiguous, writeback=wb, writeback_chunk_bytes=chunk)
         cond.prepare()
         gc.collect()
         prep_s = time.perf_counter() - t0
@@ -1709,7 +1714,7 @@ def summary_line(r: dict) -> str:
                      f"+as_tensor {vl['python_ensure_as_tensor_us']} us, evict+remap 1.5 GB {vl['evict_remap_1p5gb_ms']} ms")
     t = r.get("turbo")
     if t:
-        for mode in ("engine_layout", "reference_layout"):
+        for mode in ("engine_layout", "reference_layout", "reference_layout_full_write_back"):
             if isinstance(t.get(mode), dict):
                 parts.append(f"turbo/{mode} {t[mode]['ms_per_step']} ms/step, pcie {t[mode].get('pcie_frac')}")
     tr = r.get("train")

@@ -457,18 +457,25 @@ int sh_saveback_set_timing(sh_saveback* sb, int enable);
 int sh_saveback_clock_ns(uint64_t* ns);
 int sh_saveback_ticket_times(sh_saveback* sb, uint64_t ticket, uint64_t* out2);
 /* Save-back of the chunks that changed (no reference counterpart: the reference copies the
- * whole block back, src/stagehand/scheduler.py:1216-1226). Copies dev_src[0, bytes) into
- * host_dst (pinned) in chunks of chunk_bytes, after the caller's events (or, with
- * n_events == 0, after the work queued on `stream` now), and only the chunks whose digest
- * differs from `digests` (two uint64 per chunk, as sh_block_digest wrote them, device
- * memory): once the events have completed, the engine's worker runs sh_block_changed on
- * `digest_stream` into `changed` (pinned host memory, one byte per chunk), waits for it, and
- * issues one copy per run of changed chunks. digests == NULL copies every chunk. The caller
- * vouches that host_dst held the bytes the digests describe. All buffers stay in use until
- * the ticket completes; sh_saveback_ticket_bytes then gives the bytes copied. */
-int sh_saveback_submit_chunks(sh_saveback* sb, void* host_dst, const void* dev_src, uint64_t bytes,
-                              uint32_t chunk_bytes, const uint64_t* digests, uint8_t* changed, void* digest_stream,
-                              void* const* events, uint32_t n_events, void* stream, uint64_t* ticket);
+ * whole block back, src/stagehand/scheduler.py:1216-1226). Each region copies dev_src[0, bytes)
+ * into host_dst (pinned) in chunks of chunk_bytes, only the chunks whose digest differs from
+ * digests[2 * (first_chunk + c)], [.. + 1] (as sh_block_digest wrote them for that region,
+ * device memory). The submit queues sh_block_changed for every region on `digest_stream`, after
+ * the caller's events (or, with n_events == 0, after the work queued on `stream` now), into
+ * changed[first_chunk + c] (pinned host memory, one byte per chunk); once that has run, the
+ * engine's worker issues one copy per run of changed chunks. digests == NULL copies every chunk
+ * (ordered as sh_saveback_submit / _submit_after). The caller vouches that each host_dst held the
+ * bytes its digests describe. All buffers stay in use until the ticket completes;
+ * sh_saveback_ticket_bytes then gives the bytes copied. */
+typedef struct sh_chunk_region {
+  void* host_dst;
+  const void* dev_src;
+  uint64_t bytes;
+  uint64_t first_chunk; /* the region's first chunk in digests / changed */
+} sh_chunk_region;
+int sh_saveback_submit_chunks(sh_saveback* sb, const sh_chunk_region* regions, uint32_t n_regions, uint32_t chunk_bytes,
+                              const uint64_t* digests, uint8_t* changed, void* digest_stream, void* const* events,
+                              uint32_t n_events, void* stream, uint64_t* ticket);
 /* Waits for the ticket and gives the bytes its copies moved. */
 int sh_saveback_ticket_bytes(sh_saveback* sb, uint64_t ticket, uint64_t* bytes);
 
@@ -534,6 +541,13 @@ int sh_turbo_set_writeback(sh_turbo* t, uint32_t block, int enable);
  * hipMemcpyAsync on the engine's evict stream (a kernel on the compute units),
  * ordered on the device only. */
 int sh_turbo_set_save_back(sh_turbo* t, int sdma);
+/* Before sh_turbo_initialize (no reference counterpart): write-backs on the SDMA engine copy
+ * back only the chunks of chunk_bytes (a multiple of 16; default 1 MiB) that changed in the
+ * slot since the block's H2D: the H2D is followed by the chunk digests of the slot's copy runs
+ * on the prefetch stream (sh_block_digest), and the write-back compares them on the evict stream
+ * and copies the changed runs (sh_saveback_submit_chunks). The host region ends up holding the slot's
+ * bytes, as after the reference's full copy (engine.rs:232-262). 0: every byte is copied. */
+int sh_turbo_set_writeback_chunks(sh_turbo* t, uint32_t chunk_bytes);
 int sh_turbo_block_slot(sh_turbo* t, uint32_t block, int32_t* slot);     /* -1: none, engine.rs:375-378 */
 int sh_turbo_block_location(sh_turbo* t, uint32_t block, int* location); /* engine.rs:384-393 */
 int sh_turbo_counts(sh_turbo* t, uint32_t* blocks, uint32_t* slots, uint32_t* free_slots); /* engine.rs:380-382 */

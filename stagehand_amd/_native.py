@@ -175,8 +175,7 @@ _SIGNATURES: dict[str, list] = {
     "sh_saveback_set_timing": [_vp, _i32],
     "sh_saveback_clock_ns": [ctypes.POINTER(ctypes.c_uint64)],
     "sh_saveback_ticket_times": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
-    "sh_saveback_submit_chunks": [_vp, _vp, _vp, ctypes.c_uint64, _u32, _vp, _vp, _vp, _vp, _u32, _vp,
-                                  ctypes.POINTER(ctypes.c_uint64)],
+    "sh_saveback_submit_chunks": [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _vp, ctypes.POINTER(ctypes.c_uint64)],
     "sh_saveback_ticket_bytes": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
     "sh_block_digest": [_vp, ctypes.c_uint64, _u32, _vp, _vp],
     "sh_block_changed": [_vp, ctypes.c_uint64, _u32, _vp, _vp, _vp],
@@ -222,7 +221,11 @@ _SIGNATURES: dict[str, list] = {
     "sh_dl_free": [_vp],
     "sh_turbo_block_times": [_vp, _u32, _vp, _vp],
     "sh_turbo_trace_spans": [_vp, _vp, _u32, _vp],
+    "sh_turbo_set_writeback_chunks": [_vp, _u32],
 }
+
+# Mirror of `struct sh_chunk_region`.
+CHUNK_REGION_DTYPE = np.dtype([("host_dst", "<u8"), ("dev_src", "<u8"), ("bytes", "<u8"), ("first_chunk", "<u8")])
 
 # Mirror of `struct sh_load_request`.
 LOAD_REQUEST_DTYPE = np.dtype([

@@ -25,8 +25,9 @@
 // one stream would.
 //
 // Chunk save-backs (sh_saveback_submit_chunks): when the caller has digests of what
-// the host buffer holds (sh_digest.hip), the worker, once the fences have passed,
-// compares them with the device buffer on a stream the caller names, waits for that,
+// the host buffer holds (sh_digest.hip), the submit queues their comparison with the
+// device buffer on a stream the caller names, ordered after the caller's events, and
+// the job's fence after it; the worker, once the fence has passed, reads the flags
 // and copies back only the runs of chunks whose digests changed. Such a ticket's
 // copies are decided by the worker: waiters wait until it has set them.
 
@@ -57,6 +58,7 @@ namespace {
 struct Job {
   uint64_t id = 0;
   hipEvent_t fence = nullptr;  // none for a ticket without copies
+  hipEvent_t order = nullptr;  // a chunk job's: the caller's stream, which its comparison waits for
   std::vector<hipEvent_t> after;  // the caller's events (sh_saveback_submit_after), not owned
   std::vector<sh_copy_item> items;
   std::vector<hsa_signal_t> done;  // done[k]: 1 until items[k] has been copied
@@ -66,13 +68,10 @@ struct Job {
   // sh_saveback_submit_chunks: the worker picks the copies (items, done, copied) once the
   // fences have passed, then sets `issued`; until then waiters wait for it.
   bool chunked = false;
-  uint8_t* host_dst = nullptr;
-  const uint8_t* dev_src = nullptr;
-  uint64_t bytes = 0;
+  std::vector<sh_chunk_region> regions;
   uint32_t chunk = 0;
   const uint64_t* digests = nullptr;
   uint8_t* changed = nullptr;
-  hipStream_t digest_stream = nullptr;
   bool issued = true;  // guarded by the engine lock
 
   Job() = default;
@@ -82,6 +81,7 @@ struct Job {
     for (hsa_signal_t s : done)
       if (s.handle != 0) hsa_signal_destroy(s);
     if (fence != nullptr) (void)hipEventDestroy(fence);
+    if (order != nullptr) (void)hipEventDestroy(order);
   }
 };
 
@@ -108,7 +108,6 @@ struct sh_saveback {
   bool stop = false;
   std::atomic<bool> timing{false};  // read by the worker without the lock
   std::condition_variable issued_cv;  // a chunk job's copies were picked
-  hipEvent_t compared = nullptr;      // the worker's: end of a chunk job's digest comparison
   std::thread worker;
 };
 
@@ -130,32 +129,25 @@ void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, size
 // For a chunk job whose fences have passed: compares the chunks' digests (when given), then
 // sets the job's copies, one per run of changed chunks, with a signal each, and publishes them.
 int pick_chunks(sh_saveback* sb, Job& j, std::string& err) {
-  const uint64_t n = j.bytes / j.chunk + (j.bytes % j.chunk != 0 ? 1 : 0);
-  if (j.digests != nullptr) {
-    int st = sh::launch_block_changed(j.dev_src, j.bytes, j.chunk, j.digests, j.changed, j.digest_stream);
-    if (st != SH_OK) {
-      err = std::string("sh_block_changed: ") + sh_last_error();
-      return st;
-    }
-    hipError_t e = hipEventRecord(sb->compared, j.digest_stream);
-    if (e == hipSuccess) e = hipEventSynchronize(sb->compared);
-    if (e != hipSuccess) {
-      err = std::string("digest comparison: ") + hipGetErrorString(e);
-      return SH_ERR_HIP;
-    }
-  }
+  (void)err;
+  auto chunks_of = [&](uint64_t bytes) { return bytes / j.chunk + (bytes % j.chunk != 0 ? 1 : 0); };
+  // the comparison ran on the device before the job's fence, which has passed
   std::vector<sh_copy_item> runs;
   const volatile uint8_t* changed = j.changed;
-  for (uint64_t c = 0; c < n;) {
-    if (j.digests != nullptr && changed[c] == 0) {
-      ++c;
-      continue;
+  for (const sh_chunk_region& r : j.regions) {
+    const uint64_t n = chunks_of(r.bytes);
+    const volatile uint8_t* f = j.digests != nullptr ? changed + r.first_chunk : nullptr;
+    for (uint64_t c = 0; c < n;) {
+      if (f != nullptr && f[c] == 0) {
+        ++c;
+        continue;
+      }
+      uint64_t c1 = c + 1;
+      while (c1 < n && (f == nullptr || f[c1] != 0)) ++c1;
+      const uint64_t b = c * j.chunk, e = c1 < n ? c1 * j.chunk : r.bytes;
+      runs.push_back(sh_copy_item{(uint8_t*)r.host_dst + b, (const uint8_t*)r.dev_src + b, e - b});
+      c = c1;
     }
-    uint64_t c1 = c + 1;
-    while (c1 < n && (j.digests == nullptr || changed[c1] != 0)) ++c1;
-    const uint64_t b = c * j.chunk, e = c1 < n ? c1 * j.chunk : j.bytes;
-    runs.push_back(sh_copy_item{j.host_dst + b, j.dev_src + b, e - b});
-    c = c1;
   }
   std::vector<hsa_signal_t> sigs;
   for (size_t k = 0; k < runs.size(); ++k) {
@@ -291,11 +283,6 @@ extern "C" int sh_saveback_create(int device, sh_saveback** out) {
     hsa_shut_down();
     return sh::fail(SH_ERR_HIP, "sh_saveback_create: no CPU agent");
   }
-  e = hipEventCreateWithFlags(&sb->compared, hipEventDisableTiming);
-  if (e != hipSuccess) {
-    hsa_shut_down();
-    return sh::fail(SH_ERR_HIP, "sh_saveback_create: hipEventCreate: %s", hipGetErrorString(e));
-  }
   sh_saveback* raw = sb.release();
   raw->worker = std::thread(worker_loop, raw);
   *out = raw;
@@ -317,7 +304,6 @@ extern "C" int sh_saveback_destroy(sh_saveback* sb) {
     if (first == SH_OK) first = st;
   }
   sb->jobs.clear();  // the last references: each job's signal and fence go with it
-  if (sb->compared != nullptr) (void)hipEventDestroy(sb->compared);
   delete sb;
   hsa_shut_down();
   return first;
@@ -399,36 +385,57 @@ extern "C" int sh_saveback_submit_after(sh_saveback* sb, const sh_copy_item* ite
   return submit_job(sb, items, n, nullptr, n_events ? events : kNone, n_events, ticket);
 }
 
-extern "C" int sh_saveback_submit_chunks(sh_saveback* sb, void* host_dst, const void* dev_src, uint64_t bytes,
+extern "C" int sh_saveback_submit_chunks(sh_saveback* sb, const sh_chunk_region* regions, uint32_t n_regions,
                                          uint32_t chunk_bytes, const uint64_t* digests, uint8_t* changed,
                                          void* digest_stream, void* const* events, uint32_t n_events, void* stream,
                                          uint64_t* ticket) {
   static const char* who = "sh_saveback_submit_chunks";
   sh::clear_error();
-  if (sb == nullptr || ticket == nullptr || (n_events > 0 && events == nullptr))
+  if (sb == nullptr || ticket == nullptr || (n_regions > 0 && regions == nullptr) || (n_events > 0 && events == nullptr))
     return sh::fail(SH_ERR_INVALID, "%s: NULL argument", who);
   *ticket = 0;
-  if (bytes > 0 && (host_dst == nullptr || dev_src == nullptr)) return sh::fail(SH_ERR_INVALID, "%s: NULL buffer", who);
   if (chunk_bytes == 0 || chunk_bytes % 16 != 0)
     return sh::fail(SH_ERR_INVALID, "%s: chunk_bytes %u is not a positive multiple of 16", who, chunk_bytes);
   if (digests != nullptr && changed == nullptr) return sh::fail(SH_ERR_INVALID, "%s: digests without `changed`", who);
-  if (bytes / chunk_bytes + (bytes % chunk_bytes != 0 ? 1 : 0) > 0x7FFFFFFFull)
-    return sh::fail(SH_ERR_INVALID, "%s: too many chunks of %u bytes", who, chunk_bytes);
+  auto j = std::make_shared<Job>();
+  for (uint32_t i = 0; i < n_regions; ++i) {
+    const sh_chunk_region& r = regions[i];
+    if (r.bytes == 0) continue;
+    if (r.host_dst == nullptr || r.dev_src == nullptr)
+      return sh::fail(SH_ERR_INVALID, "%s: region %u has a NULL buffer", who, i);
+    const uint64_t n = r.bytes / chunk_bytes + (r.bytes % chunk_bytes != 0 ? 1 : 0);
+    if (n > 0x7FFFFFFFull || r.first_chunk > UINT64_MAX / 16 - n)
+      return sh::fail(SH_ERR_INVALID, "%s: region %u has too many chunks of %u bytes", who, i, chunk_bytes);
+    j->regions.push_back(r);
+  }
   for (uint32_t k = 0; k < n_events; ++k)
     if (events[k] == nullptr) return sh::fail(SH_ERR_INVALID, "%s: event %u is NULL", who, k);
-  auto j = std::make_shared<Job>();
-  if (bytes > 0) {
-    j->chunked = true;
-    j->issued = false;
-    j->host_dst = (uint8_t*)host_dst;
-    j->dev_src = (const uint8_t*)dev_src;
-    j->bytes = bytes;
-    j->chunk = chunk_bytes;
-    j->digests = digests;
-    j->changed = changed;
-    j->digest_stream = (hipStream_t)digest_stream;
+  if (j->regions.empty()) return enqueue_job(sb, j, stream, n_events ? events : nullptr, n_events, ticket);
+  j->chunked = true;
+  j->issued = false;
+  j->chunk = chunk_bytes;
+  j->digests = digests;
+  j->changed = changed;
+  if (digests == nullptr) return enqueue_job(sb, j, stream, n_events ? events : nullptr, n_events, ticket);
+  // The comparison goes on digest_stream now, after the caller's events (or after the work
+  // queued on `stream`), and the job's fence after it: it is not queued behind work that
+  // digest_stream receives later, and the worker only reads the flags.
+  hipStream_t ds = (hipStream_t)digest_stream;
+  hipError_t e = hipSuccess;
+  if (n_events > 0) {
+    for (uint32_t k = 0; k < n_events && e == hipSuccess; ++k) e = hipStreamWaitEvent(ds, (hipEvent_t)events[k], 0);
+  } else if ((hipStream_t)stream != ds) {
+    e = hipEventCreateWithFlags(&j->order, hipEventDisableTiming);  // lives with the job
+    if (e == hipSuccess) e = hipEventRecord(j->order, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ds, j->order, 0);
   }
-  return enqueue_job(sb, j, stream, n_events ? events : nullptr, n_events, ticket);
+  if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "%s: ordering the comparison: %s", who, hipGetErrorString(e));
+  for (const sh_chunk_region& r : j->regions) {
+    int st = sh::launch_block_changed(r.dev_src, r.bytes, chunk_bytes, digests + 2 * r.first_chunk,
+                                      changed + r.first_chunk, ds);
+    if (st != SH_OK) return st;
+  }
+  return enqueue_job(sb, j, digest_stream, nullptr, 0, ticket);
 }
 
 extern "C" int sh_saveback_ticket_bytes(sh_saveback* sb, uint64_t ticket, uint64_t* bytes) {

@@ -18,6 +18,11 @@
 //    draining the eviction stream first;
 //  * write-back can be switched off per block (frozen weights are not copied
 //    back to host memory on every eviction);
+//  * a write-back copies only the chunks the block changed on the device: its H2D
+//    is followed by chunk digests of the slot (on the prefetch stream), and the
+//    write-back compares them (on the evict stream) and copies the changed runs
+//    (sh_saveback_submit_chunks); the host region then holds the slot's bytes, as
+//    after the reference's full copy (sh_turbo_set_writeback_chunks; SDMA only);
 //  * write-back copies run on an SDMA engine (sh_saveback), not as
 //    hipMemcpyAsync on the evict stream: HIP runs a pinned device-to-host copy
 //    as a kernel on the compute units, and the compute kernels beside it run
@@ -59,12 +64,16 @@ struct Block {
   uint64_t d2h_ticket = 0;   // its write-back on the save-back engine (0: none pending)
   hipEvent_t t_start = nullptr, t_end = nullptr;  // timing events around the last H2D (timing mode)
   bool timed = false;
+  uint64_t* digests = nullptr;  // device: chunk digests of the block's copy runs after its last H2D
+  uint8_t* changed = nullptr;   // pinned: one byte per chunk, the write-back's comparison
+  bool digested = false;        // the digests describe this residency's slot bytes
 };
 
 // A queued write-back ticket and, in timing mode, the span that records its copy times.
 struct Pending {
   uint64_t ticket;
   int64_t span;  // index into sh_turbo::spans, -1: none
+  bool chunked;  // a write-back of changed chunks: its bytes are known once it completes
 };
 
 struct Slot {
@@ -100,6 +109,7 @@ struct sh_turbo {
   bool timing = false;
   std::vector<sh_turbo_span> spans;  // write-backs and host waits recorded in timing mode
   uint64_t bytes_h2d = 0, bytes_d2h = 0;
+  uint32_t chunk = 1u << 20;  // write-backs of changed chunks of this size (0: every byte)
 };
 
 namespace {
@@ -181,6 +191,13 @@ int reap_tickets(sh_turbo* t) {
     int st = sh_saveback_query(t->sb, tk);
     if (st == SH_ERR_NOT_READY) break;
     if (st != SH_OK) return st;
+    if (t->tickets.front().chunked) {
+      uint64_t bytes = 0;
+      st = sh_saveback_ticket_bytes(t->sb, tk, &bytes);
+      if (st != SH_OK) return st;
+      t->bytes_d2h += bytes;
+      if (span >= 0) t->spans[(size_t)span].bytes = bytes;
+    }
     if (span >= 0) {
       // the copy engine's own start and end; none when a tool replaced the copies' signals
       uint64_t times[2] = {0, 0};
@@ -220,13 +237,12 @@ int wait_ticket(sh_turbo* t, uint64_t tk, int64_t b = -1) {
   return reap_tickets(t);
 }
 
-// The write-back copies of block b out of slot s: one item for a contiguous
-// slot, else one per run of parameters contiguous on both sides.
-std::vector<sh_copy_item> writeback_items(sh_turbo* t, const Block& b, const Slot& s) {
+// The copy runs of block b in slot s as (host, device, bytes): one for a contiguous slot, else
+// one per run of parameters contiguous on both sides (the runs copy_block copies).
+std::vector<sh_copy_item> block_runs(const Block& b, const Slot& s) {
   std::vector<sh_copy_item> items;
   if (s.base) {
     if (b.extent) items.push_back({b.host, s.base, b.extent});
-    t->bytes_d2h += b.extent;
     return items;
   }
   size_t p = 0, n = b.sizes.size();
@@ -242,10 +258,38 @@ std::vector<sh_copy_item> writeback_items(sh_turbo* t, const Block& b, const Slo
       ++q;
     }
     items.push_back({host, dev, len});
-    t->bytes_d2h += len;
     p = q;
   }
   return items;
+}
+
+// The write-back copies of block b out of slot s (every byte).
+std::vector<sh_copy_item> writeback_items(sh_turbo* t, const Block& b, const Slot& s) {
+  std::vector<sh_copy_item> items = block_runs(b, s);
+  for (const sh_copy_item& it : items) t->bytes_d2h += it.bytes;
+  return items;
+}
+
+uint64_t chunks_of(uint64_t bytes, uint32_t chunk) { return bytes / chunk + (bytes % chunk != 0 ? 1 : 0); }
+
+// Chunks the digest buffers of block b need for any slot: every run is a merge of parameters,
+// each at most its aligned size.
+uint64_t chunk_capacity(const Block& b, uint32_t chunk) {
+  uint64_t n = 0;
+  for (uint64_t sz : b.sizes) n += chunks_of(align_up(sz), chunk);
+  return n;
+}
+
+// Takes the chunk digests of block b's runs in slot s on the prefetch stream, after its H2D.
+int digest_block(sh_turbo* t, Block& b, const Slot& s) {
+  uint64_t first = 0;
+  for (const sh_copy_item& r : block_runs(b, s)) {
+    int rc = sh::launch_block_digest(r.src, r.bytes, t->chunk, b.digests + 2 * first, t->prefetch);
+    if (rc != SH_OK) return rc;
+    first += chunks_of(r.bytes, t->chunk);
+  }
+  b.digested = true;
+  return SH_OK;
 }
 
 // A free slot for block b: one whose fence has passed if any, else the one
@@ -293,6 +337,11 @@ int issue_prefetch(sh_turbo* t, uint32_t b, bool from_d2h) {
   if (t->timing) SH_HIP(hipEventRecord(blk.t_start, t->prefetch));
   rc = copy_block(t, blk, s, true, t->prefetch);
   if (rc != SH_OK) return rc;
+  blk.digested = false;
+  if (blk.digests != nullptr && blk.writeback) {
+    rc = digest_block(t, blk, s);
+    if (rc != SH_OK) return rc;
+  }
   if (t->timing) {
     SH_HIP(hipEventRecord(blk.t_end, t->prefetch));
     blk.timed = true;
@@ -347,7 +396,25 @@ int async_evict(sh_turbo* t, uint32_t b) {
   SH_HIP(hipStreamWaitEvent(t->evict, t->compute_mark, 0));
   SH_HIP(hipStreamWaitEvent(t->evict, blk.h2d, 0));
   uint64_t ticket = 0;
-  if (blk.writeback && t->sb) {
+  if (blk.writeback && t->sb && blk.digested) {
+    // the slot's bytes since the H2D are digested: copy back the chunks that changed
+    std::vector<sh_chunk_region> regions;
+    uint64_t first = 0;
+    for (const sh_copy_item& r : block_runs(blk, s)) {
+      regions.push_back({r.dst, r.src, r.bytes, first});
+      first += chunks_of(r.bytes, t->chunk);
+    }
+    // compared on the evict stream, right after the block's marked compute and its H2D
+    int rc = sh_saveback_submit_chunks(t->sb, regions.data(), (uint32_t)regions.size(), t->chunk, blk.digests,
+                                       blk.changed, t->evict, nullptr, 0, t->evict, &ticket);
+    if (rc != SH_OK) return rc;
+    int64_t span = -1;
+    if (t->timing) {
+      span = (int64_t)t->spans.size();
+      t->spans.push_back({b, SH_TURBO_SPAN_WRITEBACK, 0, 0, 0});
+    }
+    t->tickets.push_back({ticket, span, true});
+  } else if (blk.writeback && t->sb) {
     std::vector<sh_copy_item> items = writeback_items(t, blk, s);
     int rc = sh_saveback_submit(t->sb, items.data(), items.size(), t->evict, &ticket);
     if (rc != SH_OK) return rc;
@@ -358,11 +425,12 @@ int async_evict(sh_turbo* t, uint32_t b) {
       span = (int64_t)t->spans.size();
       t->spans.push_back({b, SH_TURBO_SPAN_WRITEBACK, 0, 0, bytes});
     }
-    t->tickets.push_back({ticket, span});
+    t->tickets.push_back({ticket, span, false});
   } else if (blk.writeback) {
     int rc = copy_block(t, blk, s, false, t->evict);
     if (rc != SH_OK) return rc;
   }
+  blk.digested = false;
   SH_HIP(hipEventRecord(blk.d2h, t->evict));
   SH_HIP(hipEventRecord(s.fence, t->evict));
   s.fenced = true;
@@ -436,6 +504,8 @@ extern "C" int sh_turbo_destroy(sh_turbo* t) {
     if (b.d2h) (void)hipEventDestroy(b.d2h);
     if (b.t_start) (void)hipEventDestroy(b.t_start);
     if (b.t_end) (void)hipEventDestroy(b.t_end);
+    if (b.digests) (void)hipFree(b.digests);
+    if (b.changed) (void)hipHostFree(b.changed);
   }
   for (Slot& s : t->slots)  // device pointers belong to the caller
     if (s.fence) (void)hipEventDestroy(s.fence);
@@ -489,6 +559,13 @@ extern "C" int sh_turbo_initialize(sh_turbo* t, int device, uint32_t window) {
     }
     SH_HIP(hipEventCreateWithFlags(&b.h2d, hipEventDisableTiming));
     SH_HIP(hipEventCreateWithFlags(&b.d2h, hipEventDisableTiming));
+    const uint64_t nc = (t->sb && t->chunk) ? chunk_capacity(b, t->chunk) : 0;
+    if (nc > 0) {
+      SH_HIP(hipMalloc((void**)&b.digests, 16 * nc));
+      void* h = nullptr;
+      SH_HIP(hipHostMalloc(&h, nc, hipHostMallocDefault));
+      b.changed = static_cast<uint8_t*>(h);
+    }
   }
   const uint32_t w = std::min<uint32_t>(window, (uint32_t)t->blocks.size());
   for (uint32_t i = 0; i < w; ++i) {
@@ -509,6 +586,17 @@ extern "C" int sh_turbo_set_save_back(sh_turbo* t, int sdma) {
   std::lock_guard<std::mutex> g(t->mu);
   if (t->initialized) return sh::fail(SH_ERR_STATE, "set_save_back after initialize");
   t->sdma = sdma != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_turbo_set_writeback_chunks(sh_turbo* t, uint32_t chunk_bytes) {
+  sh::clear_error();
+  if (!t) return sh::fail(SH_ERR_INVALID, "sh_turbo_set_writeback_chunks: null engine");
+  if (chunk_bytes % 16 != 0)
+    return sh::fail(SH_ERR_INVALID, "sh_turbo_set_writeback_chunks: %u is not a multiple of 16", chunk_bytes);
+  std::lock_guard<std::mutex> g(t->mu);
+  if (t->initialized) return sh::fail(SH_ERR_STATE, "set_writeback_chunks after initialize");
+  t->chunk = chunk_bytes;
   return SH_OK;
 }
 

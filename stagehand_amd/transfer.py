@@ -129,18 +129,24 @@ class SaveBackEngine:
                      handles, len(events), ctypes.byref(ticket))
         return SaveBackTicket(self, ticket.value)
 
-    def submit_chunks(self, host_dst: int, dev_src: int, nbytes: int, chunk: int, digests: int, changed: int,
+    def submit_chunks(self, regions: "list[tuple[int, int, int]]", chunk: int, digests: int, changed: int,
                       digest_stream: int, events: "list[NativeEvent] | None", stream_handle: int) -> "SaveBackTicket":
-        """Copies the chunks of ``dev_src`` whose digest differs from ``digests`` (device pointer;
-        0 copies every chunk) into ``host_dst``, after ``events`` (or after the work queued so far
-        on ``stream_handle``): the worker compares them on ``digest_stream`` into ``changed``
-        (pinned, one byte per chunk). Every buffer stays in use until the ticket completes."""
+        """Copies the chunks of each region (pinned host dst, device src, bytes) whose digest differs
+        from ``digests`` (device pointer, the regions' chunks one after another; 0 copies every
+        chunk), after ``events`` (or after the work queued so far on ``stream_handle``): the worker
+        compares them on ``digest_stream`` into ``changed`` (pinned, one byte per chunk). Every
+        buffer stays in use until the ticket completes."""
+        table = np.zeros(len(regions), dtype=_native.CHUNK_REGION_DTYPE)
+        first = 0
+        for i, (dst, src, nbytes) in enumerate(regions):
+            table[i] = (dst, src, nbytes, first)
+            first += -(-nbytes // chunk)
         ticket = ctypes.c_uint64()
         evs = events or []
         handles = (ctypes.c_void_p * max(1, len(evs)))(*[ev.handle.value for ev in evs])
-        _native.call("sh_saveback_submit_chunks", self.handle, host_dst, dev_src, nbytes, chunk, digests or None,
-                     changed or None, digest_stream, handles if evs else None, len(evs), stream_handle,
-                     ctypes.byref(ticket))
+        _native.call("sh_saveback_submit_chunks", self.handle, table.ctypes.data if len(table) else None, len(table),
+                     chunk, digests or None, changed or None, digest_stream, handles if evs else None, len(evs),
+                     stream_handle, ctypes.byref(ticket))
         return SaveBackTicket(self, ticket.value, counts_bytes=True)
 
     def set_timing(self, enable: bool) -> None:
@@ -734,8 +740,8 @@ class AsyncTransferEngine:
         if (dst.numel() * dst.element_size() < nbytes or not src.is_contiguous() or not dst.is_contiguous()
                 or changed.numel() < n_chunks or digests.numel() * digests.element_size() < 16 * n_chunks):
             raise ValueError("d2h_changed: buffers do not match the chunks")
-        done = sb.submit_chunks(dst.data_ptr(), src.data_ptr(), nbytes, chunk, digests.data_ptr(), changed.data_ptr(),
-                                self._loader_unpack_stream(), after, _current_stream_handle())
+        done = sb.submit_chunks([(dst.data_ptr(), src.data_ptr(), nbytes)], chunk, digests.data_ptr(),
+                                changed.data_ptr(), self._loader_unpack_stream(), after, _current_stream_handle())
         keep = [dst, src, digests, changed]
         if after:
             keep.extend(after)

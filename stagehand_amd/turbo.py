@@ -82,6 +82,13 @@ class TransferEngine:
             raise ValueError(f"save_back must be 'sdma' or 'stream', got {engine!r}")
         _native.call("sh_turbo_set_save_back", self._handle(), int(engine == "sdma"))
 
+    def set_writeback_chunks(self, chunk_bytes: int) -> None:
+        """Before ``initialize``: SDMA write-backs copy only the chunks of ``chunk_bytes`` (default
+        1 MiB) that changed in the slot since the block's H2D (chunk digests on the device); 0
+        copies every byte, as the reference does (turbo_src/engine.rs:232-262). The host region
+        ends up the same either way."""
+        _native.call("sh_turbo_set_writeback_chunks", self._handle(), int(chunk_bytes))
+
     def initialize(self, device: int, window_size: int) -> None:
         _native.call("sh_turbo_initialize", self._handle(), int(device), int(window_size))
 
@@ -197,20 +204,24 @@ class TurboConductor:
 
     def __init__(self, model: nn.Module, block_pattern: str = r".*\.block\.\d+$", dtype: torch.dtype = torch.bfloat16,
                  device: int = 0, vram_budget_gb: float = 18.0, *, contiguous_slots: bool = True,
-                 writeback: str = "auto", save_back: str = "sdma", window: int | None = None) -> None:
+                 writeback: str = "auto", save_back: str = "sdma", window: int | None = None,
+                 writeback_chunk_bytes: int = 1 << 20) -> None:
         """``contiguous_slots=False`` gives every parameter position its own slot tensor, as
         src/stagehand/turbo.py:123-147 does (one copy per parameter); ``writeback`` is
         "auto" (copy back only blocks with trainable parameters) or "always" (as
         turbo_src/engine.rs:233-264 does); ``save_back`` is where write-backs run
         (``TransferEngine.set_save_back``); ``window`` is the number of device slots (default
         ``WINDOW``, the reference's 3, at least 3). With write-back, every prefetch into a slot
-        waits for the write-back out of it; more slots give it more time."""
+        waits for the write-back out of it; more slots give it more time. SDMA write-backs copy
+        only the chunks of ``writeback_chunk_bytes`` that changed on the device (0: every byte;
+        ``TransferEngine.set_writeback_chunks``)."""
         _native.lib()  # fail loudly without the native library
         if writeback not in ("auto", "always"):
             raise ValueError(f"writeback must be 'auto' or 'always', got {writeback!r}")
         if save_back not in ("sdma", "stream"):
             raise ValueError(f"save_back must be 'sdma' or 'stream', got {save_back!r}")
         self._save_back = save_back
+        self._writeback_chunk_bytes = int(writeback_chunk_bytes)
         self._window = self.WINDOW if window is None else int(window)
         if self._window < 3:
             # a step loads its block before it evicts the previous one, and the last block of a
@@ -260,6 +271,7 @@ class TurboConductor:
             engine.register_block([m[2] for m in meta])
             self._param_meta.append(meta)
         engine.set_save_back(self._save_back)
+        engine.set_writeback_chunks(self._writeback_chunk_bytes)
         engine.initialize(self._device_idx, self._window)
         for bi, mod in enumerate(self._block_modules):
             params = list(mod.named_parameters())
@@ -391,6 +403,8 @@ class TurboConductor:
             start, end = (int(sp["start_ns"]) - t0_ns) / 1e6, (int(sp["end_ns"]) - t0_ns) / 1e6
             if sp["kind"] == _native.TURBO_SPAN_HOST_WAIT:
                 waits.append(("slot_reuse", start, end))
+            elif sp["bytes"] == 0:
+                continue  # a write-back of changed chunks that found none: no copy
             elif sp["start_ns"] == 0:
                 untimed += 1
             else:

@@ -290,21 +290,20 @@ def test_submit_chunks_copies_the_changed_chunks(n, chunk):
     sb = eng._saveback_engine()
     unpack = eng._loader_unpack_stream()
 
-    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None,
-                         _stream())
+    region = [(host.data_ptr(), dev.data_ptr(), n)]
+    t = sb.submit_chunks(region, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None, _stream())
     assert t.copied_bytes() == 0
     hit = sorted({0, n_chunks - 1, 1, 2, n_chunks // 2 + 1} & set(range(n_chunks)))
     for c in hit:
         dev[min(c * chunk + 3, n - 1)] += 1
-    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None,
-                         _stream())
+    t = sb.submit_chunks(region, chunk, dig.data_ptr(), flags.data_ptr(), unpack, None, _stream())
     copied = t.copied_bytes()
     assert copied == sum(min(chunk, n - c * chunk) for c in hit)
     assert torch.equal(host[:n], dev.cpu()) and (host[n:] == 0xEE).all()
     np.testing.assert_array_equal(np.flatnonzero(flags.numpy()), hit)
     # without digests: every chunk, in one run
     dev.add_(3)
-    t = sb.submit_chunks(host.data_ptr(), dev.data_ptr(), n, chunk, 0, 0, unpack, None, _stream())
+    t = sb.submit_chunks(region, chunk, 0, 0, unpack, None, _stream())
     assert t.copied_bytes() == n and torch.equal(host[:n], dev.cpu())
     eng.shutdown()
 

@@ -244,16 +244,17 @@ def test_conductor_forward_matches_resident_model():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("window", [3, 4])
-def test_conductor_with_writeback_and_other_windows_matches_resident_model(window):
+@pytest.mark.parametrize("window,chunk", [(3, 0), (4, 0), (3, 1 << 20)])
+def test_conductor_with_writeback_and_other_windows_matches_resident_model(window, chunk):
     """Write-back of every block (the reference's engine) through 3 or 4 slots: outputs match the
-    resident model and the host copies are unchanged after three passes."""
+    resident model and the host copies are unchanged after three passes. Write-backs of every byte
+    move bytes back; write-backs of changed chunks move none (inference writes no weight)."""
     model = init_(TinyStack(n=6, hidden=64, mlp=4), seed=7).to(torch.bfloat16)
     model.requires_grad_(False)
     ref = init_(TinyStack(n=6, hidden=64, mlp=4), seed=7).to(device="cuda", dtype=torch.bfloat16)
     x = torch.randn(8, 64, generator=torch.Generator().manual_seed(8)).to("cuda", torch.bfloat16)
     cond = TurboConductor(model, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, writeback="always",
-                          window=window)
+                          window=window, writeback_chunk_bytes=chunk)
     cond.prepare()
     assert cond.engine.num_gpu_slots() == window
     handles = cond.install_hooks()
@@ -264,7 +265,7 @@ def test_conductor_with_writeback_and_other_windows_matches_resident_model(windo
     for o in outs:
         assert torch.equal(o.view(torch.int16), want.view(torch.int16))
     h2d, d2h = cond.engine.bytes_moved()
-    assert d2h > 0
+    assert d2h > 0 if chunk == 0 else d2h == 0
     for h in handles:
         h.remove()
     cond.shutdown()
@@ -274,14 +275,15 @@ def test_conductor_with_writeback_and_other_windows_matches_resident_model(windo
 
 @pytest.mark.gpu
 def test_trace_records_every_write_back_and_host_wait():
-    """A traced pass with write-back of every block in the reference's per-parameter layout: one
+    """A traced pass with write-back of every byte of every block in the reference's per-parameter
+    layout: one
     write-back span per evicted block with the block's bytes, timed by the copy engine after that
     block's compute began, and host waits that end after they start."""
     model = init_(TinyStack(n=6, hidden=64, mlp=4), seed=9).to(torch.bfloat16)
     model.requires_grad_(False)
     x = torch.randn(8, 64, generator=torch.Generator().manual_seed(10)).to("cuda", torch.bfloat16)
     cond = TurboConductor(model, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16, writeback="always",
-                          contiguous_slots=False)
+                          contiguous_slots=False, writeback_chunk_bytes=0)
     cond.prepare()
     handles = cond.install_hooks()
     with torch.no_grad():
@@ -371,4 +373,74 @@ def test_lookahead_behind_a_write_back_is_issued_by_the_next_step():
         for p, want in enumerate(data[i]):
             buf = (ctypes.c_uint8 * want.numel()).from_address(e.cpu_ptr(i, p))
             assert torch.equal(torch.frombuffer(buf, dtype=torch.uint8), want), (i, p)
+    e.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("contiguous", [True, False])
+def test_writebacks_copy_the_changed_chunks(contiguous):
+    """Write-backs of changed chunks: after each H2D the engine takes chunk digests of the slot, and
+    a write-back copies back only the chunks written on the device since. Two bytes change in each
+    of blocks 0, 2 and 4 (one in the first parameter past its first chunk, one in the small last
+    parameter); blocks 1 and 3 are only read. The host regions then equal the slots' bytes, exactly
+    the changed chunks were copied (per parameter in the reference's layout of one slot tensor per
+    parameter, over the whole block in a contiguous slot), and reloading carries the changes."""
+    chunk = 1 << 16
+    sizes = lambda i: [(3 << 20) + 100, 2 << 20, 5000]
+    data = _blocks(9, 5, sizes)
+    e = TransferEngine()
+    for d in data:
+        e.register_block([t.numel() for t in d])
+    e.set_save_back("sdma")
+    e.set_writeback_chunks(chunk)
+    e.initialize(torch.cuda.current_device(), 3)
+    for i, d in enumerate(data):
+        e.stage_block(i, [t.data_ptr() for t in d])
+    if contiguous:
+        nb = e.slot_bytes()
+        slots = [torch.empty(nb, dtype=torch.uint8, device="cuda") for _ in range(3)]
+        for s, t in enumerate(slots):
+            e.set_slot_buffer(s, t.data_ptr(), nb)
+    else:
+        cap = [t.numel() for t in data[0]]
+        slots = [[torch.empty(c, dtype=torch.uint8, device="cuda") for c in cap] for _ in range(3)]
+        for s, ts in enumerate(slots):
+            e.set_slot_gpu_ptrs(s, [t.data_ptr() for t in ts])
+
+    def param_view(i, p):
+        s = e.block_slot(i)
+        if contiguous:
+            off = e.param_offset(i, p)
+            return slots[s][off:off + data[i][p].numel()]
+        return slots[s][p][:data[i][p].numel()]
+
+    changed = (0, 2, 4)
+    for i in range(5):
+        e.step(i, "forward")
+        if i in changed:
+            param_view(i, 0)[70000] += 1
+            param_view(i, 2)[10] += 1
+            data[i][0][70000] += 1
+            data[i][2][10] += 1
+    e.drain()
+    _h2d, d2h = e.bytes_moved()
+    if contiguous:
+        ext = e.param_offset(0, 2) + 5120  # 5000 B rounded up to 256
+        dirty = {70000 // chunk, (e.param_offset(0, 2) + 10) // chunk}
+        per_block = sum(min(chunk, ext - c * chunk) for c in dirty)
+    else:
+        per_block = chunk + 5000  # one chunk of parameter 0, all of parameter 2
+    # blocks 0-3 were evicted by the forward steps; block 4 keeps its slot
+    assert d2h == 2 * per_block
+    for i in range(4):
+        assert e.block_location(i) == "cpu"
+        for p, want in enumerate(data[i]):
+            buf = (ctypes.c_uint8 * want.numel()).from_address(e.cpu_ptr(i, p))
+            assert torch.equal(torch.frombuffer(buf, dtype=torch.uint8), want), (i, p)
+    for i in reversed(range(5)):
+        e.step(i, "backward")
+        torch.cuda.current_stream().synchronize()
+        for p, want in enumerate(data[i]):
+            assert torch.equal(param_view(i, p).cpu(), want), (i, p)
+    e.drain()
     e.close()
