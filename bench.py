@@ -175,7 +175,7 @@ def copy_kernel_gbps(nbytes: int = 4 << 30, reps: int = 10) -> float:
     return reps * 2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9
 
 
-def digest_kernel_gbps(nbytes: int = 740 << 20, chunk: int = 1 << 20, reps: int = 20) -> dict:
+def digest_kernel_gbps(nbytes: int = 740 << 20, chunk: int = 1 << 18, reps: int = 20) -> dict:
     """Read rate of the chunk-digest kernel (sh_block_digest; the save-back comparison reads the
     same bytes) on a buffer the size of a config-5 block, timed on its stream."""
     import torch
@@ -829,7 +829,7 @@ def turbo_leg(args) -> dict:
                        "weights pinned on the host, turbo window of 3 slots, 4096 image + 512 text tokens, inference"}
     # the reference layout writes every evicted block back (engine.rs:232-262): by default only the
     # chunks changed on the device cross PCIe (the host regions end up the same); then every byte
-    legs = (("engine_layout", True, "auto", 1 << 20), ("reference_layout", False, "always", 1 << 20),
+    legs = (("engine_layout", True, "auto", 1 << 18), ("reference_layout", False, "always", 1 << 18),
             ("reference_layout_full_write_back", False, "always", 0))
     for label, contiguous, wb, chunk in legs:
         t0 = time.perf_counter()

@@ -542,7 +542,7 @@ int sh_turbo_set_writeback(sh_turbo* t, uint32_t block, int enable);
  * ordered on the device only. */
 int sh_turbo_set_save_back(sh_turbo* t, int sdma);
 /* Before sh_turbo_initialize (no reference counterpart): write-backs on the SDMA engine copy
- * back only the chunks of chunk_bytes (a multiple of 16; default 1 MiB) that changed in the
+ * back only the chunks of chunk_bytes (a multiple of 16; default 256 KiB) that changed in the
  * slot since the block's H2D: the H2D is followed by the chunk digests of the slot's copy runs
  * on the prefetch stream (sh_block_digest), and the write-back compares them on the evict stream
  * and copies the changed runs (sh_saveback_submit_chunks). The host region ends up holding the slot's

@@ -68,7 +68,7 @@ class StagehandConfig:
     # changed chunk goes unnoticed only if both 64-bit sums of its digest collide
     # (about 2^-128; one changed word is always seen). Needs the "sdma" engine.
     save_back_changed_chunks: bool = True
-    save_back_chunk_bytes: int = 1 << 20
+    save_back_chunk_bytes: int = 1 << 18
     # the host waits in before_block until the compute of the block this many
     # blocks back has finished on the device (0: never). Loads and waits are
     # device-side, so without a bound the host can queue work for many blocks

@@ -109,7 +109,7 @@ struct sh_turbo {
   bool timing = false;
   std::vector<sh_turbo_span> spans;  // write-backs and host waits recorded in timing mode
   uint64_t bytes_h2d = 0, bytes_d2h = 0;
-  uint32_t chunk = 1u << 20;  // write-backs of changed chunks of this size (0: every byte)
+  uint32_t chunk = 1u << 18;  // write-backs of changed chunks of this size (0: every byte)
 };
 
 namespace {

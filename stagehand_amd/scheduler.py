@@ -447,7 +447,7 @@ class StagehandScheduler:
         return True
 
     def _chunk_bytes(self) -> int:
-        return int(getattr(self._config, "save_back_chunk_bytes", 1 << 20))
+        return int(getattr(self._config, "save_back_chunk_bytes", 1 << 18))
 
     def _home_load_digest(self, block_id: str, module: nn.Module, layout) -> tuple[torch.Tensor, int] | None:
         """Where a module-backed load writes its chunk digests, or None for no digests.

@@ -84,7 +84,7 @@ class TransferEngine:
 
     def set_writeback_chunks(self, chunk_bytes: int) -> None:
         """Before ``initialize``: SDMA write-backs copy only the chunks of ``chunk_bytes`` (default
-        1 MiB) that changed in the slot since the block's H2D (chunk digests on the device); 0
+        256 KiB) that changed in the slot since the block's H2D (chunk digests on the device); 0
         copies every byte, as the reference does (turbo_src/engine.rs:232-262). The host region
         ends up the same either way."""
         _native.call("sh_turbo_set_writeback_chunks", self._handle(), int(chunk_bytes))
@@ -205,7 +205,7 @@ class TurboConductor:
     def __init__(self, model: nn.Module, block_pattern: str = r".*\.block\.\d+$", dtype: torch.dtype = torch.bfloat16,
                  device: int = 0, vram_budget_gb: float = 18.0, *, contiguous_slots: bool = True,
                  writeback: str = "auto", save_back: str = "sdma", window: int | None = None,
-                 writeback_chunk_bytes: int = 1 << 20) -> None:
+                 writeback_chunk_bytes: int = 1 << 18) -> None:
         """``contiguous_slots=False`` gives every parameter position its own slot tensor, as
         src/stagehand/turbo.py:123-147 does (one copy per parameter); ``writeback`` is
         "auto" (copy back only blocks with trainable parameters) or "always" (as
