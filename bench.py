@@ -955,12 +955,14 @@ def train_leg(args) -> dict:
         torch.cuda.reset_peak_memory_stats()
         h0, d0, l0 = rt.engine.bytes_h2d, rt.engine.bytes_d2h, rt.engine.loads
         rt.engine.host_wait_ms.clear()
+        rt.scheduler.fence_kinds.clear()
         t1 = time.perf_counter()
         for i in range(args.train_steps):
             step(args.train_warmup + i)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t1
         host_waits = {k: round(v / args.train_steps, 1) for k, v in sorted(rt.engine.host_wait_ms.items())}
+        fences = {k: round(v / args.train_steps, 1) for k, v in sorted(rt.scheduler.fence_kinds.items())}
         loads = rt.engine.loads - l0
         ms = wall / args.train_steps * 1e3
         h2d = (rt.engine.bytes_h2d - h0) // args.train_steps
@@ -980,7 +982,7 @@ def train_leg(args) -> dict:
             timeline["load_gap_causes"] = load_gap_causes(trace)
         res = {"ms_per_step": round(ms, 1), "h2d_bytes_per_step": h2d, "d2h_bytes_per_step": d2h, "timeline": timeline,
                "loads_per_step": round(loads / args.train_steps, 1),
-               "host_wait_ms_per_step": host_waits,
+               "host_wait_ms_per_step": host_waits, "save_back_fences_per_step": fences,
                "h2d_gbps": round(h2d / (ms * 1e-3) / 1e9, 2), "d2h_gbps": round(d2h / (ms * 1e-3) / 1e9, 2),
                "block_bytes": sum(e.size_bytes for e in rt.registry.blocks_in_order()),
                "peak_vram_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),

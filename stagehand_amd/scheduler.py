@@ -239,6 +239,8 @@ class StagehandScheduler:
         # blocks loaded since their last after_block: the load (and the gradients moved to the
         # device with it) may still be writing them, so their save-backs wait for the whole queue
         self._unsettled: set[str] = set()
+        # save-back fences taken, by kind (telemetry): the block's last use, or the whole queue and why
+        self.fence_kinds: collections.Counter = collections.Counter()
         # device memory that an eviction gave up is left out of the budget while the
         # save-back copy still holds it (the reference's synchronous copy frees it at once)
         count_as_released = getattr(budget, "count_as_released", None)
@@ -341,12 +343,18 @@ class StagehandScheduler:
         moved) and when the block was loaded again after its last hook (the load, and gradients
         moved to the device with it, write it; the eviction has ordered the current stream after
         the load). Writes through ``param.data`` do not move the counter and are not seen here."""
-        if not self._in_step or module is None or block_id in self._unsettled:
+        if not self._in_step or module is None:
+            self.fence_kinds["whole_queue_outside_step"] += 1
+            return None
+        if block_id in self._unsettled:
+            self.fence_kinds["whole_queue_loaded_since_last_use"] += 1
             return None
         versions = self._step_versions.get(block_id)
         if versions is None or versions != tuple(p._version for p in module.parameters()):
+            self.fence_kinds["whole_queue_changed_in_place"] += 1
             return None
         last = self._last_use.get(block_id)
+        self.fence_kinds["last_use"] += 1
         return [self._step_mark] if last is None else [last, self._step_mark]
 
     def _remove_grad_hooks(self) -> None:
