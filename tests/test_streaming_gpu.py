@@ -619,3 +619,59 @@ def test_changed_chunk_save_back_round_trip():
         assert torch.equal(_bits(p), _bits(w))
     rt.end_step()
     rt.shutdown()
+
+
+def test_changed_chunk_save_backs_train_bit_identically_to_full_copy_back():
+    """The config-5 shape in small, trained twice with every block evicted after every use: once
+    with save-backs of changed chunks (the default) and once copying every byte back, as the
+    reference does. Outputs, gradients, the updated LoRA weights and the frozen weights' host values
+    are bit-identical, and the changed-chunk run moved fewer bytes back."""
+    from bench_workloads import TRAIN_BLOCK_PATTERN, TrainDiT, init_train_dit_
+
+    g = torch.Generator().manual_seed(16)
+    x = torch.randn(1, 32, 256, generator=g).to(torch.bfloat16).cuda()
+    ctx = torch.randn(1, 16, 256, generator=g).to(torch.bfloat16).cuda()
+    vec = torch.randn(1, 256, generator=g).to(torch.bfloat16).cuda()
+    target = torch.randn(1, 32, 256, generator=g).cuda()
+    runs = []
+    for changed in (True, False):
+        # blocks of more than 1 MB: each one alone crosses the high watermark, so every hook evicts
+        # every block outside the prefetch window and both runs evict the same blocks
+        model = init_train_dit_(TrainDiT(depth=4, hidden=256, heads=4, mlp_ratio=2.0, rank=8), 15)
+        assert sum(p.numel() * 2 for p in model.blocks[0].parameters()) > (1 << 20)
+        base_mb = int(torch.cuda.memory_allocated() / 2**20)
+        cfg = _config(vram_high_watermark_mb=base_mb + 1, vram_low_watermark_mb=base_mb, prefetch_window_blocks=1,
+                      save_back_changed_chunks=changed, save_back_chunk_bytes=4096)
+        rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
+                                        inference_mode=False)
+        lora = [p for n, p in model.named_parameters() if "lora" in n]
+        opt = torch.optim.SGD(lora, lr=0.5, foreach=False)
+        outs, grads = [], []
+        for step in range(3):
+            xi = x.clone().requires_grad_()
+            rt.begin_step(step)
+            with rt.managed_forward(), rt.managed_backward():
+                y = model(xi, ctx, vec)
+                torch.nn.functional.mse_loss(y.float(), target).backward()
+            rt.end_step()
+            outs.append(y.detach().cpu())
+            grads.append([p.grad.detach().cpu().clone() for p in lora])
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+        torch.cuda.synchronize()
+        for i in range(len(model.blocks)):  # the last resident blocks go back too: every host value
+            if rt.residency.get_state(f"blocks.{i}").value == "gpu_ready":
+                rt.scheduler._evict_block(f"blocks.{i}", save_back=True)
+        weights = {n: p.detach().cpu().clone() for n, p in model.named_parameters()}
+        runs.append((outs, grads, weights, rt.engine.bytes_d2h, sum(m.evictions for m in rt.telemetry.history)))
+        rt.shutdown()
+    (o1, g1, w1, d1, e1), (o2, g2, w2, d2, e2) = runs
+    assert e1 == e2 and e1 > 0
+    for a, b in zip(o1, o2):
+        assert torch.equal(_bits(a), _bits(b))
+    for ga, gb in zip(g1, g2):
+        for a, b in zip(ga, gb):
+            assert torch.equal(_bits(a), _bits(b))
+    for n in w1:
+        assert torch.equal(_bits(w1[n]), _bits(w2[n])), n
+    assert d1 < d2
