@@ -221,10 +221,10 @@ class StagehandScheduler:
         # block → pinned host buffer in the block's layout, the target of its whole-block save-backs
         self._host_homes: dict[str, torch.Tensor] = {}
         # save-backs of changed chunks (config.save_back_changed_chunks): per block, the device
-        # buffer of its chunk digests, the (digests, bytes) its last load from the home buffer
-        # wrote, and the pinned byte-per-chunk flags its save-backs compare into
+        # buffer of its chunk digests, the (digests, bytes, chunk bytes) its last load from the
+        # home buffer wrote, and the pinned byte-per-chunk flags its save-backs compare into
         self._digest_bufs: dict[str, torch.Tensor] = {}
-        self._load_digests: dict[str, tuple[torch.Tensor, int]] = {}
+        self._load_digests: dict[str, tuple[torch.Tensor, int, int]] = {}
         self._changed_flags: dict[str, torch.Tensor] = {}
         # events recorded on the compute stream after each block (config.max_run_ahead_blocks)
         self._done_marks: collections.deque = collections.deque()
@@ -415,7 +415,9 @@ class StagehandScheduler:
         buffer: that buffer is then the block's bytes in the layout, so one D2H copies it into
         a pinned host buffer kept for the block (allocated at its first eviction, reused after)
         and the parameters become views of it. The next load finds pinned pieces in the
-        layout and copies them back in one DMA. Returns False to take the per-parameter path.
+        layout and copies them back in one DMA. When that load took chunk digests
+        (``_home_load_digest``), only the chunks changed on the device since are copied.
+        Returns False to take the per-parameter path.
         """
         layout, gpu = res_entry.param_layout, res_entry.gpu_tensor
         if not self._has_cuda or layout is None or gpu is None or set(names) != {n for n, *_ in layout}:
@@ -440,7 +442,7 @@ class StagehandScheduler:
         if not fresh and loaded is not None and loaded[1] == end:
             # the block was loaded from this home buffer and its digests taken then: copy back the
             # chunks that changed on the device since
-            chunk = self._chunk_bytes()
+            chunk = loaded[2]
             n_chunks = -(-end // chunk)
             flags = self._changed_flags.get(block_id)
             if flags is None or flags.numel() < n_chunks:
@@ -457,7 +459,7 @@ class StagehandScheduler:
     def _chunk_bytes(self) -> int:
         return int(getattr(self._config, "save_back_chunk_bytes", 1 << 18))
 
-    def _home_load_digest(self, block_id: str, module: nn.Module, layout) -> tuple[torch.Tensor, int] | None:
+    def _home_load_digest(self, block_id: str, module: nn.Module, layout) -> tuple[torch.Tensor, int, int] | None:
         """Where a module-backed load writes its chunk digests, or None for no digests.
 
         Digests are taken only when the load's source is exactly the block's home buffer (every
@@ -480,12 +482,13 @@ class StagehandScheduler:
             end = max(end, off + numel * dtype.itemsize)
         if end == 0 or end > home.numel():
             return None
-        n_words = 2 * -(-end // self._chunk_bytes())
+        chunk = self._chunk_bytes()
+        n_words = 2 * -(-end // chunk)
         dig = self._digest_bufs.get(block_id)
         if dig is None or dig.numel() < n_words:
             dig = torch.empty(n_words, dtype=torch.int64, device="cuda")  # two uint64 sums per chunk
             self._digest_bufs[block_id] = dig
-        return dig, end
+        return dig, end, chunk
 
     def _release_with_save_back(self, block_id: str, res_entry: ResidencyEntry, fence_before: Any) -> None:
         """The block's device buffer, about to be dropped, stays held by the whole-block save-back
@@ -1076,7 +1079,7 @@ class StagehandScheduler:
             digest = self._home_load_digest(block_id, module, layout)
             res_entry.load = self._engine.submit_block_load(
                 block_id, source, gpu_bytes, dest_on_loader_stream=True, wait_event=d2h_fence, pinned_pieces=True,
-                digest=None if digest is None else (digest[0], digest[1], self._chunk_bytes()))
+                digest=digest)
             if digest is None:
                 self._load_digests.pop(block_id, None)
             else:
