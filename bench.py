@@ -441,8 +441,9 @@ def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
         # window's blocks and their int8 staging buffers on top of it (measured:
         # window 2, watermarks 3.8 / 2.8 GB keep the peak under 6 GB while the
         # loads still run ahead of compute)
-        cfg = stagehand.StagehandConfig(pinned_pool_mb=2048, pinned_slab_mb=256, vram_high_watermark_mb=3800,
-                                        vram_low_watermark_mb=2800, prefetch_window_blocks=args.dit_prefetch,
+        high, low = (int(v) for v in getattr(args, "squareq_watermarks", "3800,2800").split(","))
+        cfg = stagehand.StagehandConfig(pinned_pool_mb=2048, pinned_slab_mb=256, vram_high_watermark_mb=high,
+                                        vram_low_watermark_mb=low, prefetch_window_blocks=args.dit_prefetch,
                                         max_inflight_transfers=args.dit_prefetch + 1, nan_inf_check=False,
                                         strict_bf16=False, telemetry_enabled=True, pinned_source_cache=pinned)
     else:
@@ -1441,6 +1442,8 @@ def main() -> int:
     ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--dit-warmup", type=int, default=2)
     ap.add_argument("--dit-prefetch", type=int, default=2)
+    ap.add_argument("--squareq-watermarks", default="3800,2800", metavar="HIGH,LOW",
+                    help="config 4: VRAM watermarks in MB under its 6 GB cap")
     ap.add_argument("--workdir", default=None, help="directory for the DiT weight files (default: system temp)")
     ap.add_argument("--dit-modes", default="staged", choices=["staged", "pinned", "both"])
     ap.add_argument("--only-dit", action="store_true", help="skip the config-2 kernel legs (profiling the DiT stream)")
