@@ -126,10 +126,10 @@ void fail_job(sh_saveback* sb, Job& j, int status, const std::string& what, size
   for (size_t k = first; k < j.done.size(); ++k) hsa_signal_subtract_screlease(j.done[k], 1);
 }
 
-// For a chunk job whose fences have passed: compares the chunks' digests (when given), then
-// sets the job's copies, one per run of changed chunks, with a signal each, and publishes them.
+// For a chunk job whose fence has passed (and with it the comparison of its digests, queued
+// before the fence): sets the job's copies, one per run of changed chunks (every chunk without
+// digests), with a signal each, and publishes them.
 int pick_chunks(sh_saveback* sb, Job& j, std::string& err) {
-  (void)err;
   auto chunks_of = [&](uint64_t bytes) { return bytes / j.chunk + (bytes % j.chunk != 0 ? 1 : 0); };
   // the comparison ran on the device before the job's fence, which has passed
   std::vector<sh_copy_item> runs;
