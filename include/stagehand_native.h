@@ -147,7 +147,7 @@ typedef struct sh_unpack_desc {
   uint32_t tile_begin; /* first tile of this descriptor */
   uint32_t ntiles;     /* tiles covering rows*cols elements */
   uint32_t lead;       /* elements before element 0 in the first tile, so that the tiles' destination
-                          spans start on 64-byte boundaries (0 when the region start allows none) */
+                          spans start on 4 KiB boundaries (0 when the region start allows none) */
   uint32_t reserved;
 } sh_unpack_desc;     /* 64 bytes, identical layout on host and device */
 

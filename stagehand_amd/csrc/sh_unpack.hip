@@ -463,6 +463,20 @@ constexpr uint32_t kMaskAll = bit(SH_KIND_I8_ROWSCALE_BF16) | bit(SH_KIND_I8_ROW
                               bit(SH_KIND_F32_BF16) | bit(SH_KIND_BF16_F32) |
                               bit(SH_KIND_COPY_BYTES) | bit(SH_KIND_ZERO_BYTES);
 
+// Reads a whole descriptor before any of its fields is tested. Left to itself the compiler
+// loads the kind, branches on it and only then loads the fields the branch uses: one more round
+// of dependent scalar loads at the start of every workgroup (tile map entry, kind, fields).
+__device__ __forceinline__ sh_unpack_desc load_desc(const sh_unpack_desc* __restrict__ p) {
+  static_assert(sizeof(sh_unpack_desc) == 64, "descriptor is 16 dwords");
+  uint32_t w[16];
+  __builtin_memcpy(w, p, sizeof w);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+s"(w[i]));  // every dword in an SGPR here
+  sh_unpack_desc d;
+  __builtin_memcpy(&d, w, sizeof d);
+  return d;
+}
+
 template <uint32_t MASK, bool HAS_ZP>
 __device__ __forceinline__ void unpack_body(const sh_unpack_desc* __restrict__ descs,
                                             const uint32_t* __restrict__ tile_map,
@@ -471,8 +485,18 @@ __device__ __forceinline__ void unpack_body(const sh_unpack_desc* __restrict__ d
                                             const float* __restrict__ zps,
                                             uint8_t* __restrict__ dst) {
   const uint32_t tile = blockIdx.x;
-  const sh_unpack_desc d = descs[tile_map[tile]];
+  const sh_unpack_desc d = load_desc(descs + tile_map[tile]);
   const uint32_t local = tile - d.tile_begin;
+  // The single-kind kernels are launched only for plans whose every descriptor has that kind
+  // (launch_tiles), so they test no kind.
+  if constexpr (MASK == kMaskDequantBf16) {
+    tile_i8<true, HAS_ZP>(d, local, src, scales, zps, dst);
+    return;
+  }
+  if constexpr (MASK == kMaskCastBf16) {
+    tile_f32_bf16(d, local, src, dst);
+    return;
+  }
   switch (d.kind) {
     case SH_KIND_I8_ROWSCALE_BF16:
       if constexpr ((MASK & bit(SH_KIND_I8_ROWSCALE_BF16)) != 0)
@@ -591,15 +615,22 @@ uint32_t dst_elem_bytes(uint32_t kind) {
   }
 }
 
-// Elements placed before element 0 in a descriptor's first tile, so that every wavefront's
-// destination span starts on a kDstAlign-byte boundary of the destination buffer (whose base
-// the caller's allocator aligns to at least that). A region that starts inside a 64-byte line
-// otherwise has every wavefront write a partial line at both ends, shared with the neighbouring
-// wavefront, which is often on another XCD: measured on MI355X, a 2.2 G-element dequant region
-// whose destination started 16 or 32 bytes into a line ran 1.9% slower, a cast 1.2% slower. The
-// lead keeps chunks in their place relative to the region (a multiple of the chunk), so a region
-// whose start allows no such lead gets none.
-constexpr uint64_t kDstAlign = 64;
+// Elements placed before element 0 in a descriptor's first tile, so that the tiles' destination
+// spans start on kDstAlign-byte boundaries of the destination buffer (whose base the caller's
+// allocator aligns to at least that), or failing that on 64-byte lines. Measured on MI355X:
+// - a region that starts inside a 64-byte line has every wavefront write a partial line at both
+//   ends, shared with the neighbouring wavefront, often on another XCD; a 2.2 G-element dequant
+//   region whose destination started 16 or 32 bytes into a line ran 1.9% slower, a cast 1.2%;
+// - line-aligned tiles still lose to tiles on 1 KiB or larger boundaries: a flat cast whose
+//   destination tiles started 512 B past a 1 KiB boundary ran 1.3% slower, at 64 B past one
+//   8.8%; on the config-2 slab, 4 KiB against 64-byte alignment raised the dequant from 6.44-6.48
+//   to 6.55-6.57 TB/s and the cast from 6.19-6.21 to 6.26-6.28.
+// The lead is below one tile for every kind (at most 4095 destination bytes), so a region gains
+// at most one tile. It keeps chunks in their place relative to the region (a multiple of the
+// chunk), so a region whose start allows no such lead gets none. 64 bytes of destination are a
+// whole number of chunks for every kind, so a region that could be put on a 64-byte line can be
+// put on a kDstAlign boundary.
+constexpr uint64_t kDstAlign = 4096;
 uint32_t lead_of(uint32_t kind, uint64_t dst_off) {
   const uint64_t ob = dst_elem_bytes(kind);
   const uint64_t mis = dst_off % kDstAlign;

@@ -118,9 +118,9 @@ def test_plan_describe_counts_and_extents():
 
 
 def test_plan_tiles_start_on_destination_lines():
-    """A region whose destination starts inside a 64-byte line gets a lead of elements before its
-    element 0, so every wavefront's destination span starts on a line; the lead is a whole number of
-    chunks (8 int8, 4 fp32, 16 bytes of copy, 32 of zero fill) or nothing."""
+    """A region whose destination starts off a 4 KiB boundary gets a lead of elements before its
+    element 0, so the tiles' destination spans start on such boundaries; the lead is a whole number
+    of chunks (8 int8, 4 fp32, 16 bytes of copy, 32 of zero fill) or nothing."""
     t_i8 = describe([(KIND_I8_ROWSCALE_BF16, 0, 0, 1, 1 << 16, 0, 0)])["tile_elems"]
     t_f32 = (1 << 20) // describe([(KIND_F32_BF16, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
     t_copy = (1 << 20) // describe([(KIND_COPY_BYTES, 0, 0, 1, 1 << 20, 0, 0)])["n_tiles"]
@@ -132,7 +132,16 @@ def test_plan_tiles_start_on_destination_lines():
     # exactly one tile of elements: a lead adds a tile, no lead keeps one
     assert tiles(KIND_I8_ROWSCALE_BF16, 16, t_i8) == 2      # lead 8 elements (16 B)
     assert tiles(KIND_I8_ROWSCALE_BF16, 48, t_i8) == 2      # lead 24
-    assert tiles(KIND_I8_ROWSCALE_BF16, 64, t_i8) == 1      # on a line already
+    assert tiles(KIND_I8_ROWSCALE_BF16, 4096, t_i8) == 1    # on a boundary already
+    assert tiles(KIND_I8_ROWSCALE_BF16, 3 * 4096, t_i8) == 1
+    assert tiles(KIND_I8_ROWSCALE_BF16, 64, t_i8) == 2      # lead 32: on a line, not on a boundary
+    assert tiles(KIND_I8_ROWSCALE_BF16, 4096 + 4080, t_i8) == 2   # lead 2040, below one tile
+    assert tiles(KIND_I8_ROWSCALE_BF16, 4096 + 4080, t_i8 - 2040) == 1
+    assert tiles(KIND_I8_ROWSCALE_BF16, 4096 + 4080, t_i8 - 2039) == 2
+    assert tiles(KIND_F32_BF16, 4088, t_f32) == 2           # lead 2044 of a 2048-element tile
+    assert tiles(KIND_F32_BF16, 4088, 4) == 1
+    assert tiles(KIND_F32_BF16, 4088, 5) == 2
+    assert tiles(KIND_F32_BF16, 8192, t_f32) == 1
     assert tiles(KIND_I8_ROWSCALE_BF16, 18, t_i8) == 1      # 9 elements: not whole chunks
     assert tiles(KIND_I8_ROWSCALE_BF16, 8, t_i8) == 1       # 4 elements: not whole chunks
     assert tiles(KIND_F32_BF16, 8, t_f32) == 2              # lead 4
