@@ -683,18 +683,27 @@ def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | Non
     ``sh_put_descs_kernel`` dispatch to the start of the last. Within it: the union of
     host-to-device copy intervals, of the unpack kernels (``sh_*``) and of all other kernels
     (the model's compute), their intersection, and, given the window's H2D bytes (the bench's
-    ``pcie_bytes_per_step`` times its steps), the H2D rate while copying."""
+    ``pcie_bytes_per_step`` times its steps), the H2D rate while copying.
+
+    A kernel trace alone (no ``memory_copy_trace.csv``) gives the compute side and the block
+    arrivals: each block load ends with its unpack kernel, launched once the block's bytes have
+    landed, so the unpack kernels' start times are the blocks' arrival times. Reported: compute
+    busy over the window, its longest idle stretches, and the arrival intervals; with the
+    window's H2D bytes, the H2D rate over the window."""
     import csv
 
-    def rows(pattern: str) -> list[dict]:
+    def rows(pattern: str, required: bool = True) -> list[dict]:
         files = sorted(trace_dir.rglob(pattern))
         if not files:
+            if not required:
+                return []
             raise FileNotFoundError(f"no {pattern} under {trace_dir}")
         with open(files[0], newline="") as fh:
             return list(csv.DictReader(fh))
 
     kernels = rows("*kernel_trace.csv")
-    copies = rows("*memory_copy_trace.csv")
+    copies = rows("*memory_copy_trace.csv", required=False)
+    copy_trace = bool(copies) or bool(sorted(trace_dir.rglob("*memory_copy_trace.csv")))
     marks = sorted((int(k["Start_Timestamp"]), int(k["End_Timestamp"])) for k in kernels
                    if k["Kernel_Name"].startswith("sh_put_descs_kernel"))
     if len(marks) < 2:
@@ -719,6 +728,30 @@ def trace_summary(trace_dir: Path, h2d_bytes: int | None, pcie_gbps: float | Non
     h2d_w, d2h_w, comp_w, unp_w = (_union(clip(x)) for x in (h2d, d2h, compute, unpack))
     ms = 1e-6
     window_ms = (w1 - w0) * ms
+    if not copy_trace:
+        import statistics
+
+        starts = sorted(a for a, b in unpack if w0 <= a < w1)
+        gaps = [(b - a) * ms for a, b in zip(starts, starts[1:])]
+        idle = sorted(((b0 - a1) * ms for (_a0, a1), (b0, _b1) in zip(comp_w, comp_w[1:])), reverse=True)
+        comp_busy = _length(comp_w) * ms
+        out = {
+            "window_ms": round(window_ms, 2),
+            "compute_kernels": sum(1 for a, b in compute if b > w0 and a < w1),
+            "compute_busy_ms": round(comp_busy, 2),
+            "compute_busy_frac": round(comp_busy / window_ms, 4) if window_ms else None,
+            "compute_idle_top_ms": [round(x, 2) for x in idle[:5]],
+            "unpack_kernels": len(starts),
+            "unpack_busy_ms": round(_length(unp_w) * ms, 2),
+            "arrival_interval_ms": ({"median": round(statistics.median(gaps), 3), "min": round(min(gaps), 3),
+                                     "max": round(max(gaps), 3)} if gaps else None),
+        }
+        if h2d_bytes:
+            out["h2d_bytes"] = int(h2d_bytes)
+            out["h2d_gbps_over_window"] = round(h2d_bytes / (window_ms * 1e-3) / 1e9, 2)
+            if pcie_gbps:
+                out["frac_of_measured_pinned_pcie_over_window"] = round(out["h2d_gbps_over_window"] / pcie_gbps, 4)
+        return out
     h2d_busy = _length(h2d_w) * ms
     comp_busy = _length(comp_w) * ms
     overlap = _intersect(h2d_w, comp_w) * ms

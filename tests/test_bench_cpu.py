@@ -61,6 +61,38 @@ def test_trace_summary_overlap_arithmetic(tmp_path):
     assert out["frac_of_measured_pinned_pcie_while_copying"] == 0.5
 
 
+def test_trace_summary_from_a_kernel_trace_alone(tmp_path):
+    """Without a memory-copy trace: compute busy, its idle stretches and the blocks' arrivals (the
+    unpack kernels' starts) in the marked window."""
+    ms = 1_000_000
+    kernels = [
+        ("sh_put_descs_kernel", 0, 1 * ms),                  # the window starts at 1 ms
+        ("sh_unpack_mixed_kernel", 1 * ms, 2 * ms),          # block 1 lands at 1 ms
+        ("Cijk_gemm", 2 * ms, 5 * ms),
+        ("sh_unpack_mixed_kernel", 4 * ms, 5 * ms),          # block 2 at 4 ms
+        ("attn_fwd", 5 * ms, 7 * ms),                        # compute 2..7, then idle 7..9
+        ("sh_dequant_i8_bf16_kernel", 8 * ms, 9 * ms),       # block 3 at 8 ms
+        ("elementwise", 9 * ms, 10 * ms),
+        ("sh_put_descs_kernel", 11 * ms, 12 * ms),           # the window ends at 11 ms
+    ]
+    with open(tmp_path / "run_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, K_FIELDS)
+        w.writeheader()
+        for i, (name, a, b) in enumerate(kernels):
+            w.writerow({"Kind": "KERNEL_DISPATCH", "Kernel_Name": name, "Dispatch_Id": i, "Start_Timestamp": a,
+                        "End_Timestamp": b})
+    out = bench.trace_summary(tmp_path, h2d_bytes=10**9, pcie_gbps=200.0)
+    assert out["window_ms"] == 10.0
+    assert out["compute_kernels"] == 3 and out["compute_busy_ms"] == 6.0
+    assert out["compute_busy_frac"] == 0.6
+    assert out["compute_idle_top_ms"] == [2.0]
+    assert out["unpack_kernels"] == 3 and out["unpack_busy_ms"] == 3.0
+    assert out["arrival_interval_ms"] == {"median": 3.5, "min": 3.0, "max": 4.0}
+    assert out["h2d_gbps_over_window"] == 100.0
+    assert out["frac_of_measured_pinned_pcie_over_window"] == 0.5
+    assert "h2d_busy_ms" not in out
+
+
 def test_trace_summary_needs_two_markers(tmp_path):
     _write(tmp_path, [("sh_put_descs_kernel", 0, 1)], [("HOST_TO_DEVICE", 0, 1)])
     with pytest.raises(ValueError):
