@@ -113,8 +113,17 @@ class SlabAllocator:
     def ensure_resident(self, slab: int, region: int, stream: int) -> "ResidentHandle":
         """Maps the region if needed; ``stream`` is the consumer's stream handle
         (``torch.cuda.current_stream().cuda_stream``)."""
+        h = self._h
+        if h is None:
+            raise RuntimeError("VMM allocator has been closed")
         out = ctypes.c_void_p()
-        _native.call("sh_vmm_ensure_resident", self._handle(), int(slab), int(region), int(stream), ctypes.byref(out))
+        fn = _native.lib().sh_vmm_ensure_resident
+        try:
+            st = fn(h, slab, region, stream, ctypes.byref(out))
+        except ctypes.ArgumentError:  # ids or stream given as another integer type
+            st = fn(h, int(slab), int(region), int(stream), ctypes.byref(out))
+        if st != _native.SH_OK:
+            _native.check(st, "sh_vmm_ensure_resident")
         return ResidentHandle(out, self)
 
     def prefetch(self, slab: int, region: int) -> None:
@@ -195,12 +204,14 @@ class ResidentHandle:
         if dtype not in _DL_DTYPES:
             raise ValueError(f"Unsupported dtype: {dtype}")
         code, bits, tdtype = _DL_DTYPES[dtype]
-        dims = np.ascontiguousarray(shape, dtype=np.int64)
+        dims = (ctypes.c_int64 * len(shape))(*shape)
         managed = ctypes.c_void_p()
-        _native.call("sh_vmm_handle_export", self._h, code, bits, dims.size, dims.ctypes.data, ctypes.byref(managed))
+        st = _native.lib().sh_vmm_handle_export(self._h, code, bits, len(shape), dims, ctypes.byref(managed))
+        if st != _native.SH_OK:
+            _native.check(st, "sh_vmm_handle_export")
         try:
             capsule = _capsule_new(managed, b"dltensor", None)
-            t = torch.utils.dlpack.from_dlpack(capsule)
+            t = torch._C._from_dlpack(capsule)  # what torch.utils.dlpack.from_dlpack calls for a capsule
         except Exception:
             _native.lib().sh_dl_free(managed)  # the export was not consumed
             raise
