@@ -213,6 +213,29 @@ def test_tensors_release_and_compute():
 
 
 @gpu
+def test_numpy_integers_for_ids_stream_and_shape():
+    """The binding's fast path passes Python ints straight to the C ABI; numpy integers (ids kept
+    in arrays, a shape from ``ndarray.shape`` arithmetic) take the converting path."""
+    import numpy as np
+
+    a = SlabAllocator(device=0)
+    mib = 1 << 20
+    s = a.create_slab(8 * mib)
+    r = a.define_region(s, 0, 4 * mib)
+    a.set_priority(s, 100)
+    h = a.ensure_resident(np.uint32(s), np.int64(r), np.int64(_stream()))
+    t = h.as_tensor("float32", [np.int64(512), np.int32(2048)])
+    assert t.shape == (512, 2048)
+    t.fill_(3.0)
+    assert float(t.sum()) == 3.0 * 512 * 2048
+    del t
+    h.release()
+    torch.cuda.synchronize()
+    a.destroy_slab(s)
+    a.close()
+
+
+@gpu
 @pytest.mark.parametrize("reader", ["pread", "mmap"])
 @pytest.mark.parametrize("mode", ["roomy", "tight", "tight_reopen"])
 def test_runtime_serves_blocks_from_vmm(tmp_path, mode, reader):
