@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 6
+#define SH_ABI_VERSION 7
 
 enum sh_status {
   SH_OK = 0,
@@ -53,12 +53,17 @@ int sh_abi_version(void);
  * vmm_src/allocator.rs:648-713, the prefetch thread's join in vmm_src/prefetch.rs:22-46).
  * Here each object's destroy call does that, and sh_shutdown ends what the library holds
  * for the whole process: it joins the shared host copy threads (at once, or when a copy
- * still running on another thread returns; they start again on the next use). It fills
- * `live` (may be NULL) with the native objects not yet destroyed, so a caller at interpreter
- * exit can check that nothing still runs when the HIP runtime is torn down. */
+ * still running on another thread returns; they start again on the next use), and, when no
+ * loader, save-back or turbo engine is alive, waits for each device that ran the library's
+ * kernels and unloads their code (loaded again on the next use). The library registers no
+ * exit-time handler of its own: a process that never calls sh_shutdown leaves the loaded code
+ * to the HIP runtime's own teardown. It fills `live` (may be NULL) with the native objects not
+ * yet destroyed, so a caller at interpreter exit can check that nothing still runs when the
+ * HIP runtime is torn down. */
 typedef struct sh_live_counts {
   uint64_t pools, loaders, savebacks, turbos, vmms, files;
-  uint64_t copy_threads; /* host copy threads still running */
+  uint64_t copy_threads;   /* host copy threads still running */
+  uint64_t kernel_devices; /* devices on which the kernels' code is still loaded */
 } sh_live_counts;
 int sh_shutdown(sh_live_counts* live);
 
@@ -202,15 +207,19 @@ int sh_unpack_cast_f32_bf16(const sh_plan* plan,
 /* No counterpart in the reference: for callers that cannot allocate device memory — code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. It does what
  * sh_plan_create + sh_unpack + sh_plan_destroy do for `descs`, with the same kernels and the
- * same results, but the plan's launch table and tile map go into a library-owned static
- * device array of SH_UNPACK_NOALLOC_SCRATCH_BYTES (8 MiB) on each GPU it runs on, held until
- * the process ends; it calls no device allocator. Descriptors reach the device as kernel
- * arguments, so nothing on the host has to outlive the call. Limits: at most
- * SH_UNPACK_NOALLOC_MAX_DESCS descriptors after the plan's splitting of oversize regions and
- * SH_UNPACK_NOALLOC_MAX_TILES tiles (config 2's dequant needs 270k, its cast 1.08 M);
- * beyond them it returns SH_ERR_INVALID. All calls on one GPU share its array and leave the
- * last call's table in it: calls ordered on one stream are safe, calls that overlap on one
- * GPU (other streams, other threads) race. */
+ * same results, but the plan's launch table and tile map go into a static device array of
+ * SH_UNPACK_NOALLOC_SCRATCH_BYTES (8 MiB) in the library's code object, one per GPU it runs on,
+ * held until sh_shutdown unloads the kernels (or the process ends); it calls no device
+ * allocator. Descriptors reach the device as kernel arguments, so nothing on the host has to
+ * outlive the call. Limits: at most SH_UNPACK_NOALLOC_MAX_DESCS descriptors after the plan's
+ * splitting of oversize regions and SH_UNPACK_NOALLOC_MAX_TILES tiles (config 2's dequant
+ * needs 270k, its cast 1.08 M); beyond them it returns SH_ERR_INVALID. All calls on one GPU
+ * share its array and leave the last call's table in it. Each call's kernels wait on the
+ * device for the previous call's on that GPU (an event recorded after every call), so calls
+ * from several streams or threads do not corrupt each other. A call made while `stream` is
+ * being captured into a graph is not ordered that way (its kernels run at the graph's
+ * replays): such replays must not overlap other calls on that GPU. The first call on a GPU
+ * loads the kernels there (as every entry point's first launch does) and creates the event. */
 #define SH_UNPACK_NOALLOC_MAX_DESCS 2048u
 #define SH_UNPACK_NOALLOC_MAX_TILES 2064384u
 #define SH_UNPACK_NOALLOC_SCRATCH_BYTES (8u << 20)

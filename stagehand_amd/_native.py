@@ -261,7 +261,7 @@ TURBO_SPAN_DTYPE = np.dtype([("block", "<u4"), ("kind", "<u4"), ("start_ns", "<u
                              ("bytes", "<u8")])
 TURBO_SPAN_WRITEBACK, TURBO_SPAN_HOST_WAIT = 0, 1
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -342,7 +342,8 @@ log = logging.getLogger(__name__)
 
 class _LiveCounts(ctypes.Structure):
     _fields_ = [(name, ctypes.c_uint64) for name in
-                ("pools", "loaders", "savebacks", "turbos", "vmms", "files", "copy_threads")]
+                ("pools", "loaders", "savebacks", "turbos", "vmms", "files", "copy_threads",
+                 "kernel_devices")]
 
 
 _tracked: list[tuple[int, int, weakref.ref, str]] = []
@@ -366,8 +367,9 @@ def track(obj: object, order: int, method: str = "close") -> None:
 
 def shutdown() -> dict[str, int]:
     """Closes every tracked native object that is still alive, then ends the library's
-    process-wide state (``sh_shutdown``: the shared copy threads are joined). Returns the
-    native objects still alive afterwards, by kind (all zero when everything closed)."""
+    process-wide state (``sh_shutdown``: the shared copy threads are joined and the kernels'
+    code is unloaded). Returns the native objects still alive afterwards, by kind (all zero
+    when everything closed)."""
     with _tracked_lock:
         items = sorted(_tracked, key=lambda t: (t[0], -t[1]))
         _tracked.clear()

@@ -35,6 +35,7 @@
 
 #include <errno.h>
 #include <fcntl.h>
+#include <pthread.h>
 #include <sys/stat.h>
 #include <sys/uio.h>
 #include <unistd.h>
@@ -140,20 +141,27 @@ int read_buffered(sh_file* f, uint8_t* dst, uint64_t off, uint64_t bytes) {
   return e;
 }
 
-// Per-thread bounce buffer for direct reads into memory that cannot take a DMA
-// (one piece plus alignment slack; freed when the thread ends).
-struct Bounce {
-  uint8_t* p = nullptr;
-  ~Bounce() { free(p); }
-  uint8_t* get() {
-    if (p == nullptr) {
-      void* q = nullptr;
-      if (posix_memalign(&q, kAlign, kPiece + 2 * kAlign) == 0) p = static_cast<uint8_t*>(q);
+// Per-thread bounce buffer for direct reads into memory that cannot take a DMA (one piece
+// plus alignment slack). It hangs off a pthread key whose destructor is libc's free, so a
+// thread's buffer is freed when the thread ends and the library registers no thread-exit
+// handler of its own (a C++ thread_local with a destructor would).
+pthread_key_t g_bounce_key;
+pthread_once_t g_bounce_once = PTHREAD_ONCE_INIT;
+bool g_bounce_key_ok = false;
+
+uint8_t* bounce_buffer() {
+  (void)pthread_once(&g_bounce_once, [] { g_bounce_key_ok = pthread_key_create(&g_bounce_key, free) == 0; });
+  if (!g_bounce_key_ok) return nullptr;
+  void* p = pthread_getspecific(g_bounce_key);
+  if (p == nullptr) {
+    if (posix_memalign(&p, kAlign, kPiece + 2 * kAlign) != 0) return nullptr;
+    if (pthread_setspecific(g_bounce_key, p) != 0) {
+      free(p);
+      return nullptr;
     }
-    return p;
   }
-};
-thread_local Bounce tls_bounce;
+  return static_cast<uint8_t*>(p);
+}
 
 constexpr uint64_t align_down(uint64_t x) { return x & ~(kAlign - 1); }
 constexpr uint64_t align_up(uint64_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
@@ -161,7 +169,7 @@ constexpr uint64_t align_up(uint64_t x) { return (x + kAlign - 1) & ~(kAlign - 1
 // Direct read of [off, off + bytes) through the bounce buffer. Returns 0, an
 // errno, or EINVAL when the file system refuses the direct read.
 int read_bounced(sh_file* f, int dfd, uint8_t* dst, uint64_t off, uint64_t bytes) {
-  uint8_t* bb = tls_bounce.get();
+  uint8_t* bb = bounce_buffer();
   if (bb == nullptr) return ENOMEM;
   while (bytes > 0) {
     const uint64_t a = align_down(off);

@@ -72,7 +72,37 @@ int run_io(const std::vector<IoPiece>& pieces, int threads);
 // the descriptor on which read-ahead advice is worth giving.
 int advice_fd(const sh_file* f);
 
-// Chunk digests (sh_digest.hip): the launches behind sh_block_digest / sh_block_changed, for
+// The library's kernels (sh_kernels.cpp): loaded per device from the embedded code objects on
+// first use, unloaded by sh_shutdown.
+enum KernelId : int {
+  kKernDequantBf16 = 0,
+  kKernDequantBf16Zp,
+  kKernCastBf16,
+  kKernMixed,
+  kKernMixedZp,
+  kKernPutDescs,
+  kKernFillTileMap,
+  kKernDigest,
+  kKernDigestCompare,
+  kKernelCount
+};
+// Launches kernel `id` of the current device: a 1-D grid of `grid` workgroups of `block`
+// work-items on `stream`; args[i] points to the i-th kernel argument.
+int launch_kernel(KernelId id, uint32_t grid, uint32_t block, hipStream_t stream, void** args, const char* who);
+// Device address of the unpack code object's `scratch` array on the current device.
+int noalloc_scratch(void** ptr, const char* who);
+// Waits for each device that has the kernels loaded, then unloads them (sh_shutdown).
+int unload_kernels();
+// Number of devices with the kernels loaded.
+int kernels_loaded();
+// Ends sh_unpack_noalloc's per-device ordering state (sh_shutdown, before unload_kernels).
+void noalloc_release();
+
+// Most chunks one digest launch may cover: one 256-work-item workgroup per chunk, in a 1-D
+// grid that stays under 2^32 work-items.
+constexpr uint64_t kMaxDigestChunks = 0xFFFFFFFFull / 256u;
+
+// Chunk digests (sh_digest.cpp): the launches behind sh_block_digest / sh_block_changed, for
 // the loader and the save-back engine.
 int launch_block_digest(const void* buf, uint64_t bytes, uint32_t chunk_bytes, uint64_t* digests, hipStream_t stream);
 int launch_block_changed(const void* buf, uint64_t bytes, uint32_t chunk_bytes, const uint64_t* digests,

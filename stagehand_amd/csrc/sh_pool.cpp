@@ -372,6 +372,16 @@ extern "C" int sh_shutdown(sh_live_counts* live) {
   // Dropping the global reference joins the copy threads here, or, when a parallel_for
   // is still running on another thread, as soon as it returns.
   CopyPool::take_global().reset();
+  // The kernels' code is unloaded only when no engine that launches them is alive (loaders
+  // launch the unpack and digests, save-back engines the comparisons, turbo engines both);
+  // otherwise it stays loaded and the library holds it until the process ends.
+  int status = SH_OK;
+  const bool launchers = sh::g_live[sh::kLiveLoader].load() != 0 || sh::g_live[sh::kLiveSaveback].load() != 0 ||
+                         sh::g_live[sh::kLiveTurbo].load() != 0;
+  if (!launchers) {
+    sh::noalloc_release();
+    status = sh::unload_kernels();
+  }
   if (live != nullptr) {
     live->pools = (uint64_t)sh::g_live[sh::kLivePool].load();
     live->loaders = (uint64_t)sh::g_live[sh::kLiveLoader].load();
@@ -380,8 +390,9 @@ extern "C" int sh_shutdown(sh_live_counts* live) {
     live->vmms = (uint64_t)sh::g_live[sh::kLiveVmm].load();
     live->files = (uint64_t)sh::g_live[sh::kLiveFile].load();
     live->copy_threads = (uint64_t)CopyPool::running_threads();
+    live->kernel_devices = (uint64_t)sh::kernels_loaded();
   }
-  return SH_OK;
+  return status;
 }
 
 extern "C" int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threads) {

@@ -404,7 +404,7 @@ extern "C" int sh_saveback_submit_chunks(sh_saveback* sb, const sh_chunk_region*
     if (r.host_dst == nullptr || r.dev_src == nullptr)
       return sh::fail(SH_ERR_INVALID, "%s: region %u has a NULL buffer", who, i);
     const uint64_t n = r.bytes / chunk_bytes + (r.bytes % chunk_bytes != 0 ? 1 : 0);
-    if (n > 0x7FFFFFFFull || r.first_chunk > UINT64_MAX / 16 - n)
+    if (n > sh::kMaxDigestChunks || r.first_chunk > UINT64_MAX / 16 - n)
       return sh::fail(SH_ERR_INVALID, "%s: region %u has too many chunks of %u bytes", who, i, chunk_bytes);
     j->regions.push_back(r);
   }

@@ -1,9 +1,10 @@
 """Per-step counters of the streaming path (fields of src/stagehand/telemetry.py:24-43).
 
 The scheduler increments the same counters at the same points as the
-reference (h2d/d2h bytes, stalls, evictions, prefetch hits/misses). This build
-adds ``copy_time_ms``: device time of the step's H2D copies and unpack
-kernels, filled in when the runtime is asked to time them.
+reference (h2d/d2h bytes, stalls, evictions, prefetch hits/misses). The
+reference declares ``copy_time_ms`` but never fills it in; here
+``record_copy_time`` fills it with the device time of the step's H2D copies
+and unpack kernels when the runtime is asked to time them.
 """
 from __future__ import annotations
 

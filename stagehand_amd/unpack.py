@@ -177,7 +177,9 @@ def unpack_noalloc(
     (``sh_unpack_noalloc``: the launch table lives in the library's static per-GPU scratch).
 
     The results equal an :class:`UnpackPlan` of the same table run with ``sh_unpack``. Calls on one
-    GPU share the scratch: calls ordered on one stream are safe, overlapping calls race."""
+    GPU share the scratch; each call's kernels wait on the device for the previous call's, from
+    any stream or thread. A call recorded into a graph is not ordered that way: replays of such a
+    graph must not overlap other calls on that GPU."""
     table = np.ascontiguousarray(descs, dtype=DESC_DTYPE)
     sp, sb = _device_ptr(src, "src")
     dp, db = _device_ptr(dst, "dst")

@@ -223,19 +223,33 @@ def test_stage_squareq_block_branches():
     zpt = rng.normal(0, 2, out_f).astype(np.float32)
     bias = rng.normal(0, 1, out_f).astype(np.float32)
     norm = rng.normal(1, 0.1, in_f).astype(np.float32)
+    # nozp: the layer has qweight and scale but no zero_point, and the weight is a module
+    # parameter: the module's value, cast (scheduler.py:272-275 fall through to 310), not a
+    # dequant with a zero point of 0. notdict: the layer is not a dict: module parameter, then,
+    # once evicted, the block's cache (scheduler.py:267, 310-322).
+    live = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float32)
+    nd_live = rng.normal(0, 0.02, (4, 5)).astype(np.float32)
+    nd_cached = rng.normal(0, 0.02, (4, 5)).astype(np.float32)
     shapes = [("lin.weight", (out_f, in_f)), ("lin.bias", (out_f,)), ("norm.weight", (in_f,)),
-              ("gone.weight", (out_f, in_f)), ("nob.bias", (out_f,)), ("evicted.weight", (3,))]
+              ("gone.weight", (out_f, in_f)), ("nob.bias", (out_f,)), ("evicted.weight", (3,)),
+              ("nozp.weight", (out_f, in_f)), ("nd.weight", (4, 5)), ("nd2.weight", (4, 5))]
     lay = oq.build_param_layout(shapes, "bfloat16")
     specs = {
         "lin.weight": oq.SquareQSpec("lin.weight", "lin", "weight", out_f, in_f, padded),
         "lin.bias": oq.SquareQSpec("lin.bias", "lin", "bias", out_f, in_f, padded),
         "gone.weight": oq.SquareQSpec("gone.weight", "missing_layer", "weight", out_f, in_f, padded),
         "nob.bias": oq.SquareQSpec("nob.bias", "nobias", "bias", out_f, in_f, padded),
+        "nozp.weight": oq.SquareQSpec("nozp.weight", "nozp", "weight", out_f, in_f, padded),
+        "nd.weight": oq.SquareQSpec("nd.weight", "notdict", "weight", 4, 5, 5),
+        "nd2.weight": oq.SquareQSpec("nd2.weight", "notdict", "weight", 4, 5, 5),
     }
-    layers = {"lin": {"qweight": q, "scale": s, "zero_point": zpt, "bias": bias}, "nobias": {}}
-    cache = {"evicted.weight": np.array([1.0, 2.0, 3.0], np.float32)}
-    buf = oq.stage_squareq_block(lay, specs, {"norm.weight", "evicted.weight"},
-                                 {"norm.weight": norm, "evicted.weight": np.zeros(0, np.float32)}, layers, cache)
+    layers = {"lin": {"qweight": q, "scale": s, "zero_point": zpt, "bias": bias}, "nobias": {},
+              "nozp": {"qweight": q, "scale": s}, "notdict": np.ones(3, np.float32)}
+    cache = {"evicted.weight": np.array([1.0, 2.0, 3.0], np.float32), "nd2.weight": nd_cached}
+    buf = oq.stage_squareq_block(
+        lay, specs, {"norm.weight", "evicted.weight", "nozp.weight", "nd.weight", "nd2.weight"},
+        {"norm.weight": norm, "evicted.weight": np.zeros(0, np.float32), "nozp.weight": live, "nd.weight": nd_live,
+         "nd2.weight": np.zeros(0, np.float32)}, layers, cache)
     region = {e.name: np.frombuffer(bytes(buf[e.offset:e.offset + e.nbytes]), np.uint16) for e in lay}
     # padded_in columns dropped, (q - zp) * s per row, rounded to bf16
     want_w = oq.bf16_rne_bits(((q[:, :in_f].astype(np.float32) - zpt[:, None]) * s[:, None]).astype(np.float32))
@@ -246,6 +260,14 @@ def test_stage_squareq_block_branches():
     assert not region["gone.weight"].any()  # missing layer, not module-backed → zero fill
     assert not region["nob.bias"].any()  # bias spec without bias → zero fill
     np.testing.assert_array_equal(region["evicted.weight"], oq.cast_f32_bf16(cache["evicted.weight"]))
+    # the module branch casts with torch's conversion, the library the reference calls
+    torch_bf16 = lambda a: torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    np.testing.assert_array_equal(region["nozp.weight"], torch_bf16(live).reshape(-1))
+    dequant_zero_zp = oq.bf16_rne_bits((q[:, :in_f].astype(np.float32) * s[:, None]).astype(np.float32))
+    assert not np.array_equal(region["nozp.weight"], dequant_zero_zp.reshape(-1))  # not a dequant with zp = 0
+    np.testing.assert_array_equal(region["nd.weight"], torch_bf16(nd_live).reshape(-1))
+    np.testing.assert_array_equal(region["nd2.weight"], torch_bf16(nd_cached).reshape(-1))
+    assert "nd.weight" in cache and "nozp.weight" in cache
 
 
 # ── oracle/torch_ref.py: the timed CPU baseline computes the checked values ─────

@@ -13,6 +13,9 @@ These tests build blocks that reach each branch, stage them through ``StagehandR
 ``oracle.squareq.stage_squareq_block`` — on the GPU through the native loader and unpack
 kernel, and on the CPU through the host staging path. A second load after an eviction,
 with some module parameters emptied and one changed, checks the cache and the live reads.
+The two module-branch fallbacks of a SquareQ weight (a layer without ``zero_point``, a layer
+that is not a dict) are also compared directly with torch's cast of the module parameter, live
+and then from the cache, independently of the oracle.
 """
 from __future__ import annotations
 
@@ -141,6 +144,21 @@ def _run(tmp_path) -> None:
     rt._scheduler.refresh_registry_snapshot()
     sched = rt._scheduler
 
+    def region(bid: str, got: np.ndarray, name: str) -> np.ndarray:
+        e = next(e for e in layouts[bid] if e.name == name)
+        return got[e.offset:e.offset + e.nbytes].view(np.uint16)
+
+    def torch_bf16(t: torch.Tensor) -> np.ndarray:
+        """The reference's module-branch cast (scheduler.py:310-322: ``param.data.to(dtype)``)."""
+        return t.detach().cpu().to(torch.bfloat16).contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+
+    # What the module branch must copy, in closed form: d.weight's layer has no zero_point and f's
+    # layer is not a dict, so both take the module parameter as it is when the block is staged,
+    # then (evicted to size 0) the value the block's first staging cached.
+    first = {bi: {k: getattr(getattr(model.blocks[bi], k.split(".")[0]), k.split(".")[1]).detach().clone()
+                  for k in ("d.weight", "f.weight", "e.bias")} for bi in range(n)}
+    expect_module = {0: {bi: dict(first[bi]) for bi in range(n)}}
+
     def load_and_check(step: int) -> None:
         rt.begin_step(step)
         for bi in range(n):
@@ -156,6 +174,8 @@ def _run(tmp_path) -> None:
                 at = int(bad[0])
                 name = next(e.name for e in layouts[bid] if e.offset <= at < e.offset + e.nbytes)
                 raise AssertionError(f"step {step} {bid}: byte {at} ({name}) differs from the oracle")
+            for name, value in expect_module[step][bi].items():
+                assert np.array_equal(region(bid, got, name), torch_bf16(value)), (step, bid, name)
             sched.after_block(bid)
         rt.end_step()
 
@@ -173,6 +193,8 @@ def _run(tmp_path) -> None:
         blk.e.bias.data = torch.empty(0)            # evicted: the block's cache holds its first value
         blk.f.weight.data = torch.empty(0)
         blk.d.weight.data = torch.randn(24, 32, generator=g)  # live: read as it is now
+    expect_module[1] = {bi: {"d.weight": model.blocks[bi].d.weight.data.clone(), "f.weight": first[bi]["f.weight"],
+                             "e.bias": first[bi]["e.bias"]} for bi in range(n)}
     load_and_check(1)
     rt.shutdown()
 

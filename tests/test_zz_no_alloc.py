@@ -5,7 +5,9 @@ scratch instead of device memory ``sh_plan_create`` allocates; the unpack kernel
 Its output must equal ``sh_unpack`` on the same descriptors and inputs byte for byte. Two calls
 in a row share the scratch: the first is config 2's full dequant (128 descriptors, 270k tiles),
 the second a smaller mixed table whose table and tile map only partly overwrite the first's.
-Limits are refused with SH_ERR_INVALID before anything is launched.
+Calls issued back to back on two streams are ordered on the device (each waits for the previous
+call's kernels before it writes the shared table), so both outputs stay exact. Limits are refused
+with SH_ERR_INVALID before anything is launched.
 """
 from __future__ import annotations
 
@@ -120,6 +122,41 @@ def test_noalloc_matches_plan_entry_point_two_calls_in_a_row():
                    torch.from_numpy(zp).cuda())
     torch.cuda.synchronize()
     assert torch.equal(again, want)
+
+
+def test_noalloc_calls_on_two_streams_do_not_corrupt_each_other():
+    """A long call (config 2's full dequant, about 1 ms of kernels) on one stream and, issued right
+    after it, a short call with another table on a second stream, then the long one again on the
+    second stream and a short one on the first. Without ordering, the second call's table writes
+    would land while the first call's unpack still reads the table."""
+    regions = config2_regions()
+    descs_a = config2_descs(regions, "dequant")
+    src_a, scales_a = config2_device_inputs(regions, "dequant", seed=5)
+    bytes_a = 2 * sum(g.numel for g in regions)
+    descs_b, slab, sc, zp, bytes_b, _ = _mixed_case(seed=6)
+    src_b, sc_b, zp_b = torch.from_numpy(slab).cuda(), torch.from_numpy(sc).cuda(), torch.from_numpy(zp).cuda()
+
+    want_a = torch.full((bytes_a,), 0xA5, dtype=torch.uint8, device="cuda")
+    want_b = torch.full((bytes_b,), 0xA5, dtype=torch.uint8, device="cuda")
+    for descs, src, sc_, zp_, want in ((descs_a, src_a, scales_a, None, want_a), (descs_b, src_b, sc_b, zp_b, want_b)):
+        plan = UnpackPlan(descs)
+        plan.run(src, want, sc_, zp_)
+        plan.close()
+    got_a1 = torch.full_like(want_a, 0xA5)
+    got_b1 = torch.full_like(want_b, 0xA5)
+    got_a2 = torch.full_like(want_a, 0xA5)
+    got_b2 = torch.full_like(want_b, 0xA5)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    unpack_noalloc(descs_a, src_a, got_a1, scales_a, None, stream=s1)
+    unpack_noalloc(descs_b, src_b, got_b1, sc_b, zp_b, stream=s2)
+    unpack_noalloc(descs_a, src_a, got_a2, scales_a, None, stream=s2)
+    unpack_noalloc(descs_b, src_b, got_b2, sc_b, zp_b, stream=s1)
+    torch.cuda.synchronize()
+    assert torch.equal(got_a1, want_a), "first long call corrupted by the call on the other stream"
+    assert torch.equal(got_b1, want_b)
+    assert torch.equal(got_a2, want_a)
+    assert torch.equal(got_b2, want_b)
 
 
 def test_noalloc_refuses_tables_beyond_its_scratch():
