@@ -67,8 +67,27 @@ class StagehandConfig:
     # bytes, as after the reference's full copy-back (scheduler.py:1216-1226); a
     # changed chunk goes unnoticed only if both 64-bit sums of its digest collide
     # (about 2^-128; one changed word is always seen). Needs the "sdma" engine.
+    # The digest is a non-cryptographic checksum, not a proof that a chunk is
+    # unchanged: a single changed 8-byte word is always seen, but for several
+    # changed words the 2^-128 figure is an argument for random changes, not a
+    # bound for structured ones. False copies every byte back, as the reference does.
     save_back_changed_chunks: bool = True
     save_back_chunk_bytes: int = 1 << 18
+    # what a module-backed block's save-back waits for inside a step:
+    # "last_use"    — the block's last hook or gradient accumulation and the
+    #                 step's start (the whole queue when a parameter's version
+    #                 counter moved since the step began, or the block was loaded
+    #                 again after its last hook). Writes that leave the version
+    #                 counter alone (through ``param.data``, e.g. from a hook, EMA
+    #                 or weight-norm code) queued after the block's last use are
+    #                 not waited for, and the host copy can miss them;
+    # "whole_queue" — everything queued on the current stream at the eviction,
+    #                 as the reference's synchronous ``param.data.to("cpu")``
+    #                 (src/stagehand/scheduler.py:1216-1226) sees it. The copy
+    #                 engine then waits for the device to reach the host, which
+    #                 runs up to max_run_ahead_blocks ahead (config 5: 1208
+    #                 against 1071 ms/step, every byte copied back).
+    save_back_fence: str = "last_use"
     # the host waits in before_block until the compute of the block this many
     # blocks back has finished on the device (0: never). Loads and waits are
     # device-side, so without a bound the host can queue work for many blocks

@@ -351,12 +351,28 @@ int issue_prefetch(sh_turbo* t, uint32_t b, bool from_d2h) {
   return SH_OK;
 }
 
+// After a failed issue_prefetch: block b goes back to where it was (its pinned region, or still
+// being written back to it) and its slot back to the free list, so no later step or wait takes
+// the slot's stale bytes, or a never-recorded H2D event, for the block's.
+void undo_prefetch(sh_turbo* t, uint32_t b, bool from_d2h) {
+  Block& blk = t->blocks[b];
+  if (blk.slot >= 0) {
+    t->slots[blk.slot].assigned = -1;
+    t->free_slots.insert(t->free_slots.begin(), blk.slot);
+  }
+  blk.slot = -1;
+  blk.location = from_d2h ? SH_TURBO_D2H : SH_TURBO_CPU;  // D2H until its event and ticket are done
+}
+
 // Issues a deferred lookahead copy (waiting on the host for the write-back it follows).
 int flush_deferred(sh_turbo* t) {
   if (t->deferred < 0) return SH_OK;
   const uint32_t b = (uint32_t)t->deferred;
+  const bool from_d2h = t->deferred_from_d2h;
   t->deferred = -1;
-  return issue_prefetch(t, b, t->deferred_from_d2h);
+  const int rc = issue_prefetch(t, b, from_d2h);
+  if (rc != SH_OK) undo_prefetch(t, b, from_d2h);
+  return rc;
 }
 
 // Starts the H2D of block b into a free slot. With may_defer, a copy that would
@@ -379,7 +395,9 @@ int async_prefetch(sh_turbo* t, uint32_t b, bool may_defer = false) {
     blk.location = SH_TURBO_H2D;
     return SH_OK;
   }
-  return issue_prefetch(t, b, from_d2h);
+  rc = issue_prefetch(t, b, from_d2h);
+  if (rc != SH_OK) undo_prefetch(t, b, from_d2h);
+  return rc;
 }
 
 // Evicts block b after the compute marked in t->compute_mark (recorded by the

@@ -204,6 +204,8 @@ class StagehandScheduler:
         reader = getattr(config, "file_reader", "mmap")
         if reader not in ("mmap", "pread", "direct"):
             raise ValueError(f"file_reader must be 'mmap', 'pread' or 'direct', got {reader!r}")
+        if getattr(config, "save_back_fence", "last_use") not in ("last_use", "whole_queue"):
+            raise ValueError(f"save_back_fence must be 'last_use' or 'whole_queue', got {config.save_back_fence!r}")
         # native weight-file reads (file_reader "pread"/"direct"): the device path only
         self._file_reader = reader if self._has_cuda else "mmap"
         self._weight_files = FileCache()
@@ -342,7 +344,12 @@ class StagehandScheduler:
         is waited for when a parameter changed in place since the step began (its version counter
         moved) and when the block was loaded again after its last hook (the load, and gradients
         moved to the device with it, write it; the eviction has ordered the current stream after
-        the load). Writes through ``param.data`` do not move the counter and are not seen here."""
+        the load). Writes through ``param.data`` do not move the counter and are not seen here;
+        ``StagehandConfig.save_back_fence="whole_queue"`` makes every save-back wait for the whole
+        queue instead."""
+        if getattr(self._config, "save_back_fence", "last_use") == "whole_queue":
+            self.fence_kinds["whole_queue_configured"] += 1
+            return None
         if not self._in_step or module is None:
             self.fence_kinds["whole_queue_outside_step"] += 1
             return None

@@ -115,3 +115,67 @@ def test_summary_line_names_every_leg():
                  "compute hidden 0.98", "train/reference_eviction 1000.0"):
         assert want in line, (want, line)
     assert "\n" not in line
+
+
+def test_summary_line_reports_config3_floor_and_weight_check():
+    r = {"value": 6200.0, "roofline": {"frac": 0.775, "kernel_ms_avg": 1.07}, "pcie": {"h2d_pinned_gbps": 57.0},
+         "dit_file": {"ms_per_step": 188.0, "pcie_bytes_per_step": 7.76e9, "streamed_gbps": 41.3,
+                      "best_mode": "staged",
+                      "staged": {"source_mode": "staged", "timeline": {"h2d_gbps_while_copying": 54.5,
+                                                                        "compute_hidden_frac": 0.58},
+                                 "floor": {"copy_at_pinned_ms": 135.5, "compute_ms": 122.1, "perfect_overlap_ms": 135.5,
+                                           "no_overlap_ms": 257.6, "frac_of_perfect_overlap": 0.7207},
+                                 "weight_check": {"resident_blocks_checked": 30, "file_params_checked": 300,
+                                                  "module_params": 60, "bytes_checked": 15.1e9, "bit_exact": True}}}}
+    line = bench.summary_line(r)
+    for want in ("config3 188.0 ms/step", "perfect-overlap floor 135.5 ms", "= 0.721 of it",
+                 "weights bit-exact True on 30 resident blocks (15.10 GB)"):
+        assert want in line, (want, line)
+
+
+def test_file_weight_check_compares_resident_buffers_with_the_shards(tmp_path):
+    """The bench's config-3 weight check on a tiny sharded model streamed on the host path: every
+    file-backed parameter of every resident block matches its shard bytes, and one flipped byte in
+    a resident buffer is caught."""
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    import stagehand_amd as stagehand
+    from stagehand_amd.config import StagehandConfig
+    from tests.streaming_models import TinyStack, init_
+
+    if torch.cuda.is_available():
+        pytest.skip("the host block path runs where there is no GPU")
+    model = init_(TinyStack(n=3, hidden=32, mlp=2)).to(torch.bfloat16)
+    shards = tmp_path / "shards"
+    shards.mkdir()
+    weight_map = {}
+    for bi, blk in enumerate(model.blocks):
+        tensors = {f"blocks.{bi}.{n}": p.detach().clone() for n, p in blk.named_parameters()}
+        save_file(tensors, str(shards / f"b{bi}.safetensors"))
+        weight_map.update({k: f"b{bi}.safetensors" for k in tensors})
+    (shards / "diffusion_pytorch_model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
+    for p in model.parameters():
+        p.requires_grad_(False)
+    cfg = StagehandConfig(pinned_pool_mb=8, pinned_slab_mb=1, vram_high_watermark_mb=200000,
+                          vram_low_watermark_mb=100000, prefetch_window_blocks=1, telemetry_enabled=False,
+                          nan_inf_check=False, strict_bf16=False)
+    rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                    inference_mode=True)
+    assert rt.convert_registry_to_file_backed_sharded(str(shards)) > 0
+    rt.begin_step(0)
+    with torch.no_grad(), rt.managed_forward():
+        model(torch.randn(2, 32).to(torch.bfloat16))
+    rt.end_step()
+    check = bench._file_weight_check(rt)
+    assert check["bit_exact"] is True and check["resident_blocks_checked"] == 3
+    assert check["file_params_checked"] > 0 and check["bytes_checked"] > 0
+    entry = rt.registry.get("blocks.1")
+    filed = {f.param_name for f in entry.file_param_specs}
+    off = next(o for name, _s, _d, o, n in entry.param_layout if name in filed and n > 2)
+    buf = rt.residency.get_entry("blocks.1").gpu_tensor
+    buf.view(torch.uint8)[off + 3] ^= 0x40
+    assert bench._file_weight_check(rt)["bit_exact"] is False
+    rt.shutdown()

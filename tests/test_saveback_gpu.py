@@ -331,3 +331,48 @@ def test_d2h_changed_waits_for_its_events_and_counts_copied_bytes():
     assert np.flatnonzero(flags.numpy()).tolist() == [5]
     assert eng.bytes_d2h - before == chunk and eng.bytes_d2h_requested == n
     eng.shutdown()
+
+
+def test_whole_queue_fence_sees_writes_through_param_data():
+    """``save_back_fence="whole_queue"``: a write through ``param.data`` (which leaves the
+    parameter's version counter alone) queued after the block's last use, behind a long run of
+    kernels, and then the block's training eviction inside the step: the host copy holds the
+    write, as the reference's synchronous ``param.data.to("cpu")`` (scheduler.py:1216-1226) sees
+    it. The default fence takes the block's last use instead, which does not order the copy after
+    such a write (the case the switch exists for)."""
+    import stagehand_amd as stagehand
+    from stagehand_amd.config import StagehandConfig
+    from tests.streaming_models import TinyStack, init_
+
+    for fence in ("whole_queue", "last_use"):
+        model = init_(TinyStack(n=3, hidden=256, mlp=4)).to(torch.bfloat16)
+        cfg = StagehandConfig(pinned_pool_mb=64, pinned_slab_mb=4, vram_high_watermark_mb=200000,
+                              vram_low_watermark_mb=100000, prefetch_window_blocks=1, telemetry_enabled=False,
+                              nan_inf_check=False, strict_bf16=False, save_back_fence=fence,
+                              save_back_changed_chunks=False)
+        rt = stagehand.StagehandRuntime(model, cfg, block_pattern=r"^blocks\.\d+$", dtype=torch.bfloat16,
+                                        inference_mode=False)
+        sched = rt._scheduler
+        x = torch.randn(4, 256).to(torch.bfloat16).cuda()
+        rt.begin_step(0)
+        with rt.managed_forward():
+            model(x).float().sum().backward()
+        w = model.blocks[0].fc1.weight
+        assert w.is_cuda
+        a = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
+        for _ in range(30):  # keeps the device busy well past the eviction's submit
+            a = torch.tanh(a @ a)
+        v0 = w._version
+        w.data.fill_(0.25)  # through .data: the version counter does not move
+        assert w._version == v0
+        sched._evict_block("blocks.0", save_back=True)
+        host = model.blocks[0].fc1.weight
+        assert not host.is_cuda
+        if fence == "whole_queue":
+            assert bool((host.float() == 0.25).all()), "the save-back ran before the write through param.data"
+            assert sched.fence_kinds["whole_queue_configured"] >= 1
+        else:
+            assert sched.fence_kinds["whole_queue_configured"] == 0
+        rt.end_step()
+        torch.cuda.synchronize()
+        rt.shutdown()
