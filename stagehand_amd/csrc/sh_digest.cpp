@@ -12,17 +12,22 @@
 //
 // The digest of chunk [b, e) of a buffer is a pair of 64-bit sums, over every 8-byte word
 // w_j of the chunk (j = byte offset in the buffer / 8; the last partial word of the buffer is
-// zero-padded), of
-//   A: mix_a(w_j ^ (j * kKeyA))    and    B: mix_b(w_j ^ (j * kKeyB) ^ kKeyC),
-// modulo 2^64. mix_a is the output function of SplitMix64 (Steele, Lea and Flood, "Fast
-// splittable pseudorandom number generators", OOPSLA 2014); mix_b has the same
-// xorshift-multiply form with other shifts and the odd multipliers of MurmurHash3's 64-bit
-// finalizer. Each step is a bijection of 64-bit words (an xorshift by at least half the width,
-// a multiply by an odd constant, an xor with a key fixed by the position), so a change of one
-// word changes both sums. Several changed words leave a chunk's digest unchanged only if their
-// mixed differences cancel in both sums at once, which for two unrelated mixers is a chance of
-// about 2^-128. The sums commute, so the digest does not depend on how the words are spread
-// over threads.
+// zero-padded), with l_j and h_j its low and high 32-bit halves and k_j = j * kKey mod 2^32, of
+//   A: f(l_j ^ k_j) + f(h_j ^ k_j) * 2^32    and    B: g(l_j ^ k_j) + g(h_j ^ k_j) * 2^32,
+// modulo 2^64. f is the 32-bit finalizer of MurmurHash3 (Appleby); g is "lowbias32" (Wellons,
+// hash-prospector), the same xorshift-multiply form with other shifts and odd multipliers. Each
+// step of either is a bijection of 32-bit words (an xorshift by at least half the width, a
+// multiply by an odd constant), so each word's term in A (two 32-bit mixes side by side) is a
+// bijection of the keyed word, and a change of one word changes both sums. Several changed
+// words leave a chunk's digest unchanged only if their terms' differences cancel in both sums at
+// once, which for two unrelated mixers is a chance of about 2^-128 for random changes; it is a
+// checksum, not a bound for structured changes. The sums commute, so the digest does not depend
+// on how the words are spread over threads.
+//
+// 32-bit mixers, not 64-bit ones: the kernel is bound by its vector ALU, and a 64-bit multiply
+// is three multiply instructions (v_mad_u64_u32 and two v_mul_lo_u32) against one. Measured on
+// MI355X over a 740 MiB block: 64-bit SplitMix64/Murmur3 mixers 0.147-0.151 ms (5.1-5.3 TB/s);
+// these 0.139-0.142 ms (5.45-5.58 TB/s), and with non-temporal loads 0.126-0.127 ms (6.1 TB/s).
 
 #include <hip/hip_runtime.h>
 

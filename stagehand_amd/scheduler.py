@@ -1136,6 +1136,8 @@ class StagehandScheduler:
     # ── eviction ─────────────────────────────────────────────────────
 
     def _run_eviction(self, ignore_cooldown: bool = False) -> None:
+        """Evicts by score down to the low watermark (scheduler.py:1128-1182); each eviction is
+        followed by the save-back backlog bound."""
         cooldown = 0 if ignore_cooldown else self._policy.eviction_cooldown_steps
         candidates = self._residency.eviction_candidates(current_step=self._current_step, cooldown_steps=cooldown)
         protected: set[str] = set()

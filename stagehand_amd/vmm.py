@@ -59,9 +59,29 @@ _DL_DTYPES: dict[str, tuple[int, int, torch.dtype]] = {
     "float8_e4m3fn": (1, 8, torch.float8_e4m3fn),
 }
 
-_capsule_new = ctypes.pythonapi.PyCapsule_New
-_capsule_new.restype = ctypes.py_object
-_capsule_new.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
+_from_dlpack = torch._C._from_dlpack  # what torch.utils.dlpack.from_dlpack calls for a capsule
+_fast_mod = None
+
+
+def _fast():
+    """The CPython binding of the hot path (``_lib/_sh_vmm``, built with the library): one C call
+    for ensure_resident and one for the DLPack export, as the reference's pyo3 binding
+    (vmm_src/python.rs:66-221). It links the library loaded by ``_native``."""
+    global _fast_mod
+    if _fast_mod is None:
+        import importlib.util
+
+        from stagehand_amd import build_native
+
+        _native.lib()
+        path = build_native.python_binding_path()
+        if not path.exists():
+            raise _native.NativeLibraryError(f"{path} is missing; build with python -m stagehand_amd.build_native")
+        spec = importlib.util.spec_from_file_location("stagehand_amd._sh_vmm", str(path))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _fast_mod = mod
+    return _fast_mod
 
 _available: bool | None = None
 
@@ -92,6 +112,9 @@ class SlabAllocator:
         h = ctypes.c_void_p()
         _native.call("sh_vmm_create", int(device), 0 if ceiling_mb is None else int(ceiling_mb) << 20, ctypes.byref(h))
         self._h = h
+        self._hv: int | None = h.value  # the same pointer as a plain int, for the compiled binding
+        self._ensure = _fast().ensure
+        self._export = _fast().export
         self.device = int(device)
         _native.track(self, _native.CLOSE_ENGINE)
 
@@ -113,18 +136,19 @@ class SlabAllocator:
     def ensure_resident(self, slab: int, region: int, stream: int) -> "ResidentHandle":
         """Maps the region if needed; ``stream`` is the consumer's stream handle
         (``torch.cuda.current_stream().cuda_stream``)."""
-        h = self._h
+        h = self._hv
         if h is None:
             raise RuntimeError("VMM allocator has been closed")
-        out = ctypes.c_void_p()
-        fn = _native.lib().sh_vmm_ensure_resident
         try:
-            st = fn(h, slab, region, stream, ctypes.byref(out))
-        except ctypes.ArgumentError:  # ids or stream given as another integer type
-            st = fn(h, int(slab), int(region), int(stream), ctypes.byref(out))
-        if st != _native.SH_OK:
-            _native.check(st, "sh_vmm_ensure_resident")
-        return ResidentHandle(out, self)
+            r = self._ensure(h, slab, region, stream)
+        except TypeError:  # ids or stream given as another integer type (numpy, bool)
+            r = self._ensure(h, int(slab), int(region), int(stream or 0))
+        if r < 0:
+            _native.check(-r, "sh_vmm_ensure_resident")
+        handle = ResidentHandle.__new__(ResidentHandle)
+        handle._h = r
+        handle._alloc = self
+        return handle
 
     def prefetch(self, slab: int, region: int) -> None:
         _native.call("sh_vmm_prefetch", self._handle(), int(slab), int(region))
@@ -163,6 +187,7 @@ class SlabAllocator:
         if self._h is not None:
             _native.lib().sh_vmm_destroy(self._h)
             self._h = None
+            self._hv = None
 
     def __del__(self) -> None:
         try:
@@ -172,10 +197,13 @@ class SlabAllocator:
 
 
 class ResidentHandle:
-    """Keeps a region mapped while held (vmm_src/python.rs:111-267)."""
+    """Keeps a region mapped while held (vmm_src/python.rs:111-267). ``_h`` is the native handle
+    pointer as an int."""
 
-    def __init__(self, handle: ctypes.c_void_p, allocator: SlabAllocator) -> None:
-        self._h = handle
+    __slots__ = ("_h", "_alloc", "__weakref__")
+
+    def __init__(self, handle: int, allocator: SlabAllocator) -> None:
+        self._h = int(handle.value if isinstance(handle, ctypes.c_void_p) else handle)
         self._alloc = allocator  # keeps the Python allocator object alive while handles exist
 
     @property
@@ -199,23 +227,18 @@ class ResidentHandle:
 
     def as_tensor(self, dtype: str, shape: list[int]) -> torch.Tensor:
         """A device tensor over the region (DLPack); it keeps the region mapped until it is freed."""
-        if self._h is None:
+        h = self._h
+        if h is None:
             raise RuntimeError("Handle already released")
-        if dtype not in _DL_DTYPES:
+        spec = _DL_DTYPES.get(dtype)
+        if spec is None:
             raise ValueError(f"Unsupported dtype: {dtype}")
-        code, bits, tdtype = _DL_DTYPES[dtype]
-        dims = (ctypes.c_int64 * len(shape))(*shape)
-        managed = ctypes.c_void_p()
-        st = _native.lib().sh_vmm_handle_export(self._h, code, bits, len(shape), dims, ctypes.byref(managed))
-        if st != _native.SH_OK:
-            _native.check(st, "sh_vmm_handle_export")
-        try:
-            capsule = _capsule_new(managed, b"dltensor", None)
-            t = torch._C._from_dlpack(capsule)  # what torch.utils.dlpack.from_dlpack calls for a capsule
-        except Exception:
-            _native.lib().sh_dl_free(managed)  # the export was not consumed
-            raise
-        return t.view(tdtype) if t.dtype != tdtype else t
+        code, bits, tdtype = spec
+        cap = self._alloc._export(h, code, bits, shape)
+        if type(cap) is int:
+            _native.check(-cap, "sh_vmm_handle_export")
+        t = _from_dlpack(cap)  # an unconsumed capsule frees its export when it is collected
+        return t if t.dtype is tdtype else t.view(tdtype)
 
     def release(self) -> None:
         if self._h is None:

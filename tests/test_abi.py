@@ -254,3 +254,20 @@ def test_noalloc_entry_point_refuses_tables_beyond_its_scratch():
     assert lib.sh_unpack_noalloc(many.ctypes.data, len(many), None, 0, None, None, 0, None, 0,
                                  None) == _native.SH_ERR_INVALID
     assert b"descriptors" in lib.sh_last_error()
+
+
+def test_vmm_python_binding_loads_and_reports_statuses():
+    """The compiled VMM hot-path binding (``_lib/_sh_vmm``) links the same library as the ctypes
+    handle: a NULL allocator or handle comes back as the negated SH_ERR_INVALID, with the message in
+    the library's thread-local last error; 64-bit ids are refused before the call."""
+    from stagehand_amd import vmm
+
+    m = vmm._fast()
+    assert m.ensure(0, 1, 2, 0) == -_native.SH_ERR_INVALID
+    assert "sh_vmm_ensure_resident" in _native.last_error()
+    assert m.export(0, 4, 16, [3, 4]) == -_native.SH_ERR_INVALID
+    assert "sh_vmm_handle_export" in _native.last_error()
+    with pytest.raises(ValueError):
+        m.ensure(0, 1 << 40, 2, 0)
+    with pytest.raises(ValueError):
+        m.export(0, 4, 16, [1] * 17)

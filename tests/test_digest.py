@@ -3,7 +3,7 @@ of save-backs that copy back only the chunks a block changed on the device.
 
 The digest has no counterpart in the reference (which copies every block back whole,
 src/stagehand/scheduler.py:1216-1226); what has to hold is that a changed chunk is seen. The CPU
-tests pin the host function to the definition in ``sh_digest.hip`` (restated with numpy below),
+tests pin the host function to the definition in ``sh_digest.cpp`` (restated with numpy below),
 and check that changing any one byte changes exactly the digest of the chunk holding it. The GPU
 tests check that the device kernels compute the host function's digests and flags.
 """
@@ -15,27 +15,32 @@ import pytest
 from stagehand_amd import _native
 
 M64 = (1 << 64) - 1
-KEY_A, KEY_B, KEY_C = 0x9E3779B97F4A7C15, 0xC2B2AE3D27D4EB4F, 0x165667B19E3779F9
+KEY = 0x9E3779B9
 
 
-def _mix(z: np.ndarray, s1: int, m1: int, s2: int, m2: int, s3: int) -> np.ndarray:
-    z = (z ^ (z >> np.uint64(s1))) * np.uint64(m1)
-    z = (z ^ (z >> np.uint64(s2))) * np.uint64(m2)
-    return z ^ (z >> np.uint64(s3))
+def _mix32(x: np.ndarray, s1: int, m1: int, s2: int, m2: int, s3: int) -> np.ndarray:
+    x = (x ^ (x >> np.uint32(s1))) * np.uint32(m1)
+    x = (x ^ (x >> np.uint32(s2))) * np.uint32(m2)
+    return x ^ (x >> np.uint32(s3))
 
 
 def digest_np(buf: np.ndarray, chunk: int) -> np.ndarray:
-    """The digest as sh_digest.hip defines it: per chunk, the sums mod 2^64 over its 8-byte words
-    w_j (j = byte offset / 8, the last word zero-padded) of mix_a(w_j ^ j*KA) and
-    mix_b(w_j ^ j*KB ^ KC)."""
+    """The digest as sh_digest.cpp defines it: per chunk, the sums mod 2^64 over its 8-byte words
+    w_j (j = byte offset / 8, the last word zero-padded; l, h its 32-bit halves, k = j*KEY mod
+    2^32) of f(l^k) + f(h^k)*2^32 and g(l^k) + g(h^k)*2^32, with f MurmurHash3's fmix32 and g
+    lowbias32."""
     n = buf.size
     padded = np.zeros(-(-n // 8) * 8, np.uint8)
     padded[:n] = buf
-    words = padded.view("<u8").astype(np.uint64)
-    j = np.arange(words.size, dtype=np.uint64)
+    halves = padded.view("<u4").astype(np.uint32).reshape(-1, 2)
+    j = np.arange(halves.shape[0], dtype=np.uint64)
+    k = ((j * np.uint64(KEY)) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    lo, hi = halves[:, 0] ^ k, halves[:, 1] ^ k
     with np.errstate(over="ignore"):
-        a = _mix(words ^ (j * np.uint64(KEY_A)), 30, 0xBF58476D1CE4E5B9, 27, 0x94D049BB133111EB, 31)
-        b = _mix(words ^ (j * np.uint64(KEY_B)) ^ np.uint64(KEY_C), 33, 0xFF51AFD7ED558CCD, 29, 0xC4CEB9FE1A85EC53, 32)
+        f = [_mix32(v, 16, 0x85EBCA6B, 13, 0xC2B2AE35, 16).astype(np.uint64) for v in (lo, hi)]
+        g = [_mix32(v, 16, 0x7FEB352D, 15, 0x846CA68B, 16).astype(np.uint64) for v in (lo, hi)]
+    a = f[0] | (f[1] << np.uint64(32))
+    b = g[0] | (g[1] << np.uint64(32))
     n_chunks = -(-n // chunk)
     out = np.zeros(2 * n_chunks, np.uint64)
     per = chunk // 8
@@ -43,6 +48,33 @@ def digest_np(buf: np.ndarray, chunk: int) -> np.ndarray:
         out[2 * c] = int(a[c * per:(c + 1) * per].astype(object).sum()) & M64
         out[2 * c + 1] = int(b[c * per:(c + 1) * per].astype(object).sum()) & M64
     return out
+
+
+def test_mixers_match_their_published_values():
+    """fmix32 and lowbias32 at known points: fmix32(0) = 0, and both are the published functions
+    (values computed from their definitions in exact integer arithmetic)."""
+    def ref(x, s1, m1, s2, m2, s3):
+        x ^= x >> s1
+        x = (x * m1) & 0xFFFFFFFF
+        x ^= x >> s2
+        x = (x * m2) & 0xFFFFFFFF
+        return x ^ (x >> s3)
+
+    xs = np.array([0, 1, 2, 0xFFFFFFFF, 0x12345678, 0x80000000], np.uint32)
+    with np.errstate(over="ignore"):
+        got_f = _mix32(xs, 16, 0x85EBCA6B, 13, 0xC2B2AE35, 16)
+        got_g = _mix32(xs, 16, 0x7FEB352D, 15, 0x846CA68B, 16)
+    assert [int(v) for v in got_f] == [ref(int(x), 16, 0x85EBCA6B, 13, 0xC2B2AE35, 16) for x in xs]
+    assert [int(v) for v in got_g] == [ref(int(x), 16, 0x7FEB352D, 15, 0x846CA68B, 16) for x in xs]
+    assert int(got_f[0]) == 0 and int(got_f[1]) == 0x514E28B7  # MurmurHash3 fmix32(1)
+
+
+def test_mixers_are_bijections_on_a_sample():
+    """Invertibility on a sample of 2^20 inputs: no two map to the same output."""
+    xs = np.arange(1 << 20, dtype=np.uint32) * np.uint32(0x9E3779B1)
+    with np.errstate(over="ignore"):
+        for params in ((16, 0x85EBCA6B, 13, 0xC2B2AE35, 16), (16, 0x7FEB352D, 15, 0x846CA68B, 16)):
+            assert np.unique(_mix32(xs, *params)).size == xs.size
 
 
 def digest_host(buf: np.ndarray, chunk: int) -> np.ndarray:
@@ -148,3 +180,22 @@ def test_device_digest_and_flags_match_the_host(n, chunk):
     expect = np.zeros(n_chunks, np.uint8)
     expect[hit] = 1
     np.testing.assert_array_equal(flags[:n_chunks].numpy(), expect)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("offset", [1, 4, 8, 12])
+def test_device_digest_of_a_buffer_at_any_byte_offset(offset):
+    """The kernel reads 16-byte words at any alignment of the buffer's start."""
+    import torch
+
+    n, chunk = (3 << 20) + 21, 1 << 18
+    g = torch.Generator(device="cuda").manual_seed(offset)
+    base = torch.randint(0, 256, (n + 64,), dtype=torch.uint8, device="cuda", generator=g)
+    dev = base[offset:offset + n]
+    n_chunks = -(-n // chunk)
+    dig = torch.zeros(2 * n_chunks, dtype=torch.int64, device="cuda")
+    lib = _native.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.sh_block_digest(dev.data_ptr(), n, chunk, dig.data_ptr(), stream) == _native.SH_OK
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dig.cpu().numpy().view(np.uint64), digest_host(dev.cpu().numpy(), chunk))
