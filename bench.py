@@ -1149,11 +1149,15 @@ def vmm_latency_leg(args) -> dict:
     return out
 
 
-def _vmm_run(args, src: Path, ceiling_mb: int | None = None) -> dict:
+def _vmm_run(args, src: Path, ceiling_mb: int | None = None, reactivate: bool = False) -> dict:
     """Config-3 DiT served from the VMM backend: every block registered in one slab,
     filled from the sharded safetensors on first use (native loads), then resident
     in mapped device memory under the default ceiling, or under ``ceiling_mb``, which
-    evicts and refills regions every step."""
+    evicts and refills regions every step. An eviction lowers the slab's watermark to the
+    evicted region (vmm_src/eviction.rs:130-131), after which the reference serves the blocks
+    above it by block swap; with ``reactivate`` the model is activated again before every step
+    (``VmmManager.activate_model``, which re-opens the watermark), so every step evicts and
+    re-maps regions through the VMM path."""
     import gc
 
     import torch
@@ -1183,6 +1187,8 @@ def _vmm_run(args, src: Path, ceiling_mb: int | None = None) -> dict:
     rt._vmm_before_block = counted
 
     def step(i: int):
+        if reactivate:
+            rt.vmm.activate_model("dit")
         rt.begin_step(i)
         with torch.no_grad(), rt.managed_forward():
             out = model(img, txt, vec)
@@ -1200,6 +1206,7 @@ def _vmm_run(args, src: Path, ceiling_mb: int | None = None) -> dict:
     served = {"vmm": 0, "swap": 0}
     st0 = rt.vmm.stats()
     h2d0 = rt.engine.bytes_h2d
+    torch.cuda.reset_peak_memory_stats()
     t1 = time.perf_counter()
     for i in range(args.dit_steps):
         out = step(1 + args.dit_warmup + i)
@@ -1229,7 +1236,10 @@ def _vmm_run(args, src: Path, ceiling_mb: int | None = None) -> dict:
            "evictions_per_step": (st1["evictions"] - st0["evictions"]) / args.dit_steps,
            "maps_per_step": (st1["maps"] - st0["maps"]) / args.dit_steps,
            "refill_bytes_per_step": int(h2d),
-           "refill_gbps": round(h2d / (ms * 1e-3) / 1e9, 2)}
+           "refill_gbps": round(h2d / (ms * 1e-3) / 1e9, 2),
+           "reactivated_every_step": reactivate,
+           # torch's allocations (block-swap buffers, activations) beside the mapped regions
+           "peak_torch_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2)}
     if getattr(args, "pcie_peak_gbps", None):
         res["refill_frac_of_measured_pcie"] = round(res["refill_gbps"] / args.pcie_peak_gbps, 4)
     log(f"dit/vmm: {res}")
@@ -1466,6 +1476,8 @@ def dit_leg(kind: str, args) -> dict:
         res["vmm"] = _vmm_run(args, src)
         log("dit/file: served from the VMM backend under a 19.2 GB ceiling (regions evicted and refilled)")
         res["vmm_tight"] = _vmm_run(args, src, ceiling_mb=19200)
+        log("dit/file: VMM under a 19.2 GB ceiling, the model activated again before every step")
+        res["vmm_tight_reactivated"] = _vmm_run(args, src, ceiling_mb=19200, reactivate=True)
     shutil.rmtree(workdir, ignore_errors=True)
     return res
 
@@ -1804,6 +1816,11 @@ def summary_line(r: dict) -> str:
     if isinstance(vt, dict) and "ms_per_step" in vt:
         parts.append(f"vmm 19.2 GB ceiling {vt['ms_per_step']} ms/step, {vt['evictions_per_step']} evictions/step, "
                      f"refill {vt['refill_gbps']} GB/s")
+    vr = g(r, "dit_file", "vmm_tight_reactivated")
+    if isinstance(vr, dict) and "ms_per_step" in vr:
+        bs = vr.get("blocks_served_per_step") or {}
+        parts.append(f"vmm 19.2 GB re-activated {vr['ms_per_step']} ms/step, {vr['evictions_per_step']} evictions + "
+                     f"{vr['maps_per_step']} maps/step, {bs.get('vmm')} blocks from VMM, {bs.get('swap')} swapped")
     vl = r.get("vmm_latency")
     if isinstance(vl, dict) and "native_ensure_ns" in vl:
         parts.append(f"vmm ensure {vl['native_ensure_ns']} ns native, {vl['python_ensure_us']} us python, "
