@@ -57,9 +57,10 @@ int sh_abi_version(void);
  * loader, save-back or turbo engine is alive, waits for each device that ran the library's
  * kernels and unloads their code (loaded again on the next use). The library registers no
  * exit-time handler of its own: a process that never calls sh_shutdown leaves the loaded code
- * to the HIP runtime's own teardown. It fills `live` (may be NULL) with the native objects not
- * yet destroyed, so a caller at interpreter exit can check that nothing still runs when the
- * HIP runtime is torn down. */
+ * to the HIP runtime's own teardown. No other call of the library may run while sh_shutdown
+ * does (a launch racing the unload would use freed code). It fills `live` (may be NULL) with the
+ * native objects not yet destroyed, so a caller at interpreter exit can check that nothing still
+ * runs when the HIP runtime is torn down. */
 typedef struct sh_live_counts {
   uint64_t pools, loaders, savebacks, turbos, vmms, files;
   uint64_t copy_threads;   /* host copy threads still running */

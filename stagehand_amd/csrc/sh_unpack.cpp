@@ -308,8 +308,8 @@ int launch(const sh_plan* plan, const void* src, size_t src_bytes, const float* 
 // event recorded after the last call's launches. Every call first makes its stream wait for
 // that event, so its writes to the device's scratch array start only after the previous call's
 // kernels have read it, whichever streams or threads the calls come from (on one stream the
-// wait costs nothing on the device). Nothing here has a destructor: the table is never freed (it holds at
-// most the largest plan seen) and the events end in sh_shutdown.
+// wait costs nothing on the device). Nothing here has a destructor: the table is never freed (it
+// holds at most the largest plan seen) and the events end in sh_shutdown.
 constexpr int kMaxDevices = 64;
 struct NoallocDevice {
   hipEvent_t done = nullptr;
