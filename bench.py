@@ -456,6 +456,7 @@ def _dit_config(kind: str, args, pinned: bool, reader: str = "mmap"):
                                         telemetry_enabled=True, pinned_source_cache=pinned, file_reader=reader)
     if getattr(args, "run_ahead", None) is not None:
         cfg.max_run_ahead_blocks = args.run_ahead
+        cfg.max_run_ahead_blocks_inference = args.run_ahead
     cfg.telemetry_file = None
     return cfg
 
@@ -629,6 +630,7 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     b0 = rt.engine.bytes_h2d
+    rt.engine.host_wait_ms.clear()
     trace_marker(args)
     t1 = time.perf_counter()
     for i in range(args.dit_steps):
@@ -639,10 +641,14 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
     sent = rt.engine.bytes_h2d - b0
     ms = wall / args.dit_steps * 1e3
     hist = rt.telemetry.history[-args.dit_steps:]
+    host_waits = {k: round(v / args.dit_steps, 1) for k, v in sorted(rt.engine.host_wait_ms.items())}
     # one more step with device timing of every load and compute span (not part of the timed steps)
     rt.engine.start_trace()
     step(args.dit_warmup + args.dit_steps)
-    timeline = timeline_stats(rt.engine.stop_trace(), getattr(args, "pcie_peak_gbps", None))
+    trace = rt.engine.stop_trace()
+    timeline = timeline_stats(trace, getattr(args, "pcie_peak_gbps", None))
+    if trace["loads"]:
+        timeline["load_gap_causes"] = load_gap_causes(trace)
     check = None
     if layers is not None:
         # every Linear of every resident block: its streamed weight and bias against the torch
@@ -682,6 +688,7 @@ def _dit_run(kind: str, args, src: Path, layers, pinned: bool, reader: str = "mm
         "pinned_image_gb": round(rt.engine.pinned_image_bytes / 1e9, 2),
         "stall_ms_per_step": round(sum(m.stall_time_ms for m in hist) / len(hist), 2),
         "evictions_per_step": sum(m.evictions for m in hist) / len(hist),
+        "host_wait_ms_per_step": host_waits,
         "weight_check": check,
         "out_finite": bool(torch.isfinite(out.float()).all()),
         "timeline": timeline,
@@ -1000,7 +1007,8 @@ def train_leg(args) -> dict:
                                         nan_inf_check=False, strict_bf16=False, telemetry_enabled=True,
                                         frozen_host_copies=fhc, save_back_engine=args.save_back,
                                         save_back_changed_chunks=changed,
-                                        **({} if args.run_ahead is None else {"max_run_ahead_blocks": args.run_ahead}))
+                                        **({} if args.run_ahead is None else {"max_run_ahead_blocks": args.run_ahead}),
+                                        **({} if args.backlog_mb is None else {"save_back_backlog_mb": args.backlog_mb}))
         cfg.telemetry_file = None
         rt = stagehand.StagehandRuntime(model, cfg, block_pattern=TRAIN_BLOCK_PATTERN, dtype=torch.bfloat16,
                                         inference_mode=False)
@@ -1571,7 +1579,10 @@ def main() -> int:
     ap.add_argument("--release-accounting", default="on", choices=["on", "off"],
                     help="config 5: off counts save-back-held memory as used (A/B of the eviction loop)")
     ap.add_argument("--run-ahead", type=int, default=None,
-                    help="config 5: StagehandConfig.max_run_ahead_blocks (default: the config's)")
+                    help="StagehandConfig.max_run_ahead_blocks (training) and max_run_ahead_blocks_inference "
+                         "(the DiT and VMM legs) (default: the config's)")
+    ap.add_argument("--backlog-mb", type=int, default=None,
+                    help="config 5: StagehandConfig.save_back_backlog_mb (default: the gap between the watermarks)")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     args = ap.parse_args()

@@ -88,16 +88,30 @@ class StagehandConfig:
     #                 runs up to max_run_ahead_blocks ahead (config 5: 1208
     #                 against 1071 ms/step, every byte copied back).
     save_back_fence: str = "last_use"
+    # device memory that evicted blocks' save-backs in flight may still hold
+    # before the eviction loop waits for the oldest of them (None: the gap
+    # between the watermarks, so that allocated memory stays under the high
+    # watermark plus that gap)
+    save_back_backlog_mb: int | None = None
     # the host waits in before_block until the compute of the block this many
     # blocks back has finished on the device (0: never). Loads and waits are
     # device-side, so without a bound the host can queue work for many blocks
     # ahead of the device, and every evicted block still read by queued work
     # keeps its memory; the reference blocks the host in every load instead.
-    # 12 was measured best on configs 3 and 5: with fewer, the host stalls at the
-    # forward/backward turn, where the next loads are several resident blocks away,
-    # and the copy engine idles (config 3: 215 -> 189 ms/step, config 5 with frozen
-    # host copies: 1028 -> 984 ms/step, peak VRAM unchanged).
+    # 12 was measured best on config 5 (training): with fewer, the host stalls at
+    # the forward/backward turn, where the next loads are several resident blocks
+    # away, and the copy engine idles (with frozen host copies: 1028 -> 984 ms/step,
+    # peak VRAM unchanged); with more, evicted blocks whose save-backs still wait
+    # for queued work hold more memory.
     max_run_ahead_blocks: int = 12
+    # the same bound in inference. Inference saves nothing back, so the budget
+    # already sees every buffer that queued work still holds, and the bound only
+    # keeps the host from reaching the next non-resident block early enough to
+    # issue its load while the device computes a run of resident blocks. Measured
+    # on config 3 (run-ahead 12 / 16 / 24 / 32 / 57: 188 / 181 / 168 / 163 / 159
+    # ms/step) and config 4 (211.4 ms/step at 12, 24 and 57), peak VRAM and
+    # evictions unchanged; at 57 the host never waited on it.
+    max_run_ahead_blocks_inference: int = 64
     # scheduling policy
     policy: str = "static"
     prefetch_window_blocks: int = 3

@@ -622,16 +622,22 @@ class StagehandScheduler:
 
     # ── per-block hooks ──────────────────────────────────────────────
 
+    def _run_ahead_limit(self) -> int:
+        """``max_run_ahead_blocks`` in training, ``max_run_ahead_blocks_inference`` in inference."""
+        if self._inference_mode:
+            return int(getattr(self._config, "max_run_ahead_blocks_inference", 0))
+        return int(getattr(self._config, "max_run_ahead_blocks", 0))
+
     def _bound_run_ahead(self) -> None:
-        """Host wait for the compute of the block ``max_run_ahead_blocks`` back."""
-        limit = getattr(self._config, "max_run_ahead_blocks", 0)
+        """Host wait for the compute of the block ``_run_ahead_limit()`` back."""
+        limit = self._run_ahead_limit()
         while limit > 0 and len(self._done_marks) >= limit:
             mark = self._done_marks.popleft()
             with self._host_wait("run_ahead"):
                 mark.synchronize()
 
     def _mark_block_done(self) -> None:
-        if self._has_cuda and getattr(self._config, "max_run_ahead_blocks", 0) > 0:
+        if self._has_cuda and self._run_ahead_limit() > 0:
             ev = NativeEvent()
             ev.record(torch.cuda.current_stream().cuda_stream)
             self._done_marks.append(ev)
@@ -1168,11 +1174,14 @@ class StagehandScheduler:
         wait = getattr(self._engine, "wait_releasing", None)
         if wait is None:
             return
-        high = getattr(self._budget, "high_watermark_mb", None)
-        low = getattr(self._budget, "low_watermark_mb", None)
-        if high is None or low is None:
-            return
-        wait(int((high - low) * 1024 * 1024))
+        allowed_mb = getattr(self._config, "save_back_backlog_mb", None)
+        if allowed_mb is None:
+            high = getattr(self._budget, "high_watermark_mb", None)
+            low = getattr(self._budget, "low_watermark_mb", None)
+            if high is None or low is None:
+                return
+            allowed_mb = high - low
+        wait(int(allowed_mb * 1024 * 1024))
 
     def _release_device_buffer(self, res_entry: ResidencyEntry) -> None:
         """Drop the block's device buffer; an unfinished load is waited for on the device first."""
