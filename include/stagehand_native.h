@@ -324,7 +324,14 @@ int sh_host_copy_batch(const sh_copy_item* items, size_t n, int threads);
  * A native worker thread that performs a block load end to end: gather the
  * block's parameter bytes into a pinned slab (multi-threaded host copy), H2D
  * the slab on the loader's copy stream, and, with a plan, unpack it into the
- * destination on the loader's unpack stream. Replaces the synchronous host
+ * destination. The unpack and the chunk digests (post-copy work) are queued by
+ * the first call that needs them: sh_loader_stream_wait queues them on its
+ * stream behind a device wait on the copy; sh_loader_query (once the copy has
+ * landed), sh_loader_sync, sh_loader_release, sh_loader_ticket_times and
+ * sh_loader_destroy queue them on the loader's unpack stream after the copy
+ * has landed. No loader stream waits on the device for a copy still queued:
+ * HIP runs the streams that share a hardware queue in the order their work was
+ * queued, so such a wait could hold back the compute stream. Replaces the synchronous host
  * staging + copy + host wait of src/stagehand/scheduler.py:953-1031,
  * src/stagehand/transfer.py:108-143 / 193-217 and the prefetch half of
  * turbo_src/engine.rs:202-282.
@@ -393,8 +400,8 @@ typedef struct sh_load_request {
   uint64_t saveback_ticket;
   /* Optional digests of the destination once written (no reference counterpart; for
    * sh_saveback_submit_chunks): sh_block_digest of dst[0, digest_bytes) in chunks of
-   * digest_chunk bytes into `digest` (device memory), on the loader's unpack stream, before
-   * the load counts as done. */
+   * digest_chunk bytes into `digest` (device memory), as post-copy work, before the load
+   * counts as done. */
   uint64_t* digest;
   uint64_t digest_bytes;
   uint32_t digest_chunk;
@@ -406,14 +413,17 @@ int sh_loader_create(sh_pool* pool, int copy_threads, sh_loader** out);
 int sh_loader_destroy(sh_loader* loader);
 int sh_loader_streams(sh_loader* loader, void** copy_stream, void** unpack_stream);
 int sh_loader_submit(sh_loader* loader, const sh_load_request* req, void* wait_stream, uint64_t* ticket);
-/* SH_OK once the destination is written, SH_ERR_NOT_READY before. */
+/* SH_OK once the destination is written, SH_ERR_NOT_READY before. Queues the
+ * post-copy work on the unpack stream once the copy has landed. */
 int sh_loader_query(sh_loader* loader, uint64_t ticket);
 /* Makes `stream` wait for the load on the device (the host waits only until
- * the worker has issued it). */
+ * the worker has issued it). The first call for a ticket with post-copy work
+ * queues that work on `stream`, behind a device wait on the copy. */
 int sh_loader_stream_wait(sh_loader* loader, uint64_t ticket, void* stream);
 /* Host waits until the destination is written. */
 int sh_loader_sync(sh_loader* loader, uint64_t ticket);
-/* Forgets a ticket (waits for its device work first). */
+/* Forgets a ticket (waits for its device work first, post-copy work included:
+ * the destination and digests are written on return). */
 int sh_loader_release(sh_loader* loader, uint64_t ticket);
 /* Timing of later submissions (no reference counterpart; the per-block copy
  * and unpack GB/s telemetry): when enabled, each ticket's copy-start,

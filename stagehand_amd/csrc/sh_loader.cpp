@@ -1,7 +1,7 @@
 // Block loader: a native worker that stages a block's parameter bytes into a
 // pinned slab, copies the slab to the device on a copy stream and (for SquareQ
-// or fp32 sources) runs the unpack kernel on a second stream, all fenced by
-// HIP events.
+// or fp32 sources, or with chunk digests) runs the unpack / digest kernels once
+// the copy has landed, all fenced by HIP events.
 //
 // This replaces the synchronous host path of the reference's block loads:
 //   _stage_block_to_host       src/stagehand/scheduler.py:953-1031 (pool.acquire,
@@ -20,10 +20,25 @@
 //                   and read its file ranges (pread / O_DIRECT) on the same
 //                   threads,
 //                   copy stream: wait `ready`, H2D slab → staging (or → dst),
-//                   record `copied`; release the slab after `copied`;
-//                   unpack stream: wait `copied`, launch the plan, record `done`.
+//                   record `copied`; release the slab after `copied`.
+//                   Without post-copy work (no plan, no digest) `done` is
+//                   recorded right there.
+//   post-copy work: the plan's unpack and the chunk digests, then `done`, are
+//                   queued by the first caller that needs them:
+//                   sh_loader_stream_wait queues them on the caller's stream
+//                   behind a device wait on `copied`; sh_loader_query,
+//                   sh_loader_sync, sh_loader_release, sh_loader_ticket_times
+//                   and sh_loader_destroy queue them on the loader's unpack
+//                   stream once `copied` has completed (query only looks;
+//                   the others wait on the host).
 //   caller thread : sh_loader_stream_wait(ticket, compute stream) makes the
-//                   compute stream wait for `done` without blocking the host.
+//                   compute stream wait for the load without blocking the host.
+// No stream of the loader therefore holds a device wait for a copy that is
+// still queued. HIP maps its streams onto a few hardware queues
+// (GPU_MAX_HW_QUEUES, 4 by default) and work of two streams that share one
+// runs in the order it was queued: a wait for the next block's copy, queued
+// on a loader stream that shares its hardware queue with the compute stream,
+// held back every kernel queued behind it until that copy landed.
 // The worker owns the host-side staging, so the Python hook thread never
 // copies weight bytes and never waits for a copy to finish. When it starts a
 // ticket, the buffered file ranges of that ticket and of the one queued behind
@@ -82,6 +97,8 @@ struct Ticket {
   uint64_t* digest = nullptr;  // chunk digests of dst once written (sh_block_digest)
   uint64_t digest_bytes = 0;
   uint32_t digest_chunk = 0;
+  // the plan's unpack and the digests (then `done`) are still to be queued (launch_post)
+  bool post_pending = false;
 };
 
 }  // namespace
@@ -297,34 +314,47 @@ int run_request(sh_loader* L, Ticket& t, std::string& err) {
   }
   e = hipEventRecord(t.copied, L->copy_stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord(copied)");
-  int st = SH_OK;
-  if (t.plan == nullptr && t.digest == nullptr) {
+  if (!t.post_pending) {
     e = hipEventRecord(t.done, L->copy_stream);
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
-    return SH_OK;
   }
-  e = hipStreamWaitEvent(L->unpack_stream, t.copied, 0);
-  if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(copied)");
-  if (t.plan != nullptr) {
+  return SH_OK;
+}
+
+// Queues ticket `t`'s post-copy work (the plan's unpack, the chunk digests) on `stream` behind a
+// device wait on `copied`, and records `done` after it. Called with L->mu held, once per ticket,
+// after the worker has issued it. On failure the ticket fails, and `done` still marks the end of
+// whatever was queued.
+int launch_post(sh_loader* L, Ticket& t, hipStream_t stream, const char* who) {
+  t.post_pending = false;
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  hipError_t e = prev == L->device ? hipSuccess : hipSetDevice(L->device);
+  int st = SH_OK;
+  if (e == hipSuccess) e = hipStreamWaitEvent(stream, t.copied, 0);
+  if (e != hipSuccess) {
+    st = sh::fail(SH_ERR_HIP, "%s: ordering the unpack after the copy: HIP error %d (%s)", who, (int)e,
+                  hipGetErrorString(e));
+  }
+  if (st == SH_OK && t.plan != nullptr) {
     const uint8_t* stg = (const uint8_t*)t.staging;
     const float* scales = t.scale_off >= 0 ? (const float*)(stg + t.scale_off) : nullptr;
     const float* zps = t.zp_off >= 0 ? (const float*)(stg + t.zp_off) : nullptr;
-    st = sh_unpack(t.plan, t.staging, t.staging_bytes, scales, zps, t.n_scale, t.dst, t.dst_bytes, L->unpack_stream);
-    if (st != SH_OK) {
-      err = sh_last_error();
-      return st;
-    }
+    st = sh_unpack(t.plan, t.staging, t.staging_bytes, scales, zps, t.n_scale, t.dst, t.dst_bytes, stream);
   }
-  if (t.digest != nullptr) {
-    st = sh::launch_block_digest(t.dst, t.digest_bytes, t.digest_chunk, t.digest, L->unpack_stream);
-    if (st != SH_OK) {
-      err = sh_last_error();
-      return st;
-    }
+  if (st == SH_OK && t.digest != nullptr)
+    st = sh::launch_block_digest(t.dst, t.digest_bytes, t.digest_chunk, t.digest, stream);
+  e = hipEventRecord(t.done, stream);
+  if (st == SH_OK && e != hipSuccess)
+    st = sh::fail(SH_ERR_HIP, "%s: hipEventRecord(done): HIP error %d (%s)", who, (int)e, hipGetErrorString(e));
+  if (prev >= 0 && prev != L->device) (void)hipSetDevice(prev);
+  if (st != SH_OK) {
+    t.status = st;
+    t.error = sh_last_error();
+    t.state = TicketState::Failed;
+    L->issued_cv.notify_all();
   }
-  e = hipEventRecord(t.done, L->unpack_stream);
-  if (e != hipSuccess) return hip_fail(e, "hipEventRecord(done)");
-  return SH_OK;
+  return st;
 }
 
 // Queues POSIX_FADV_WILLNEED for the buffered file ranges of `t` (once per
@@ -362,18 +392,17 @@ void worker_loop(sh_loader* L) {
     std::string err;
     const int st = run_request(L, *t, err);
     if (st != SH_OK) {
-      // Chunks copied before the failure may still be landing in the destination, and kernels
-      // queued on the unpack stream may still read it: mark the end of both so that releasing
-      // the ticket waits for them.
+      // Chunks copied before the failure may still be landing in the destination: mark their
+      // end so that releasing the ticket waits for them (no post-copy work was queued).
       (void)hipEventRecord(t->copied, L->copy_stream);
-      (void)hipStreamWaitEvent(L->unpack_stream, t->copied, 0);
-      (void)hipEventRecord(t->done, L->unpack_stream);
+      (void)hipEventRecord(t->done, L->copy_stream);
     }
     {
       std::lock_guard<std::mutex> lk(L->mu);
       t->status = st;
       t->error = err;
       t->state = st == SH_OK ? TicketState::Issued : TicketState::Failed;
+      if (st != SH_OK) t->post_pending = false;
       t->pieces.clear();
       t->pieces.shrink_to_fit();
       t->ranges.clear();
@@ -417,6 +446,28 @@ int wait_issued(sh_loader* L, uint64_t id, std::unique_lock<std::mutex>& lk, Tic
                     it->second.error.c_str());
   *out = &it->second;
   return SH_OK;
+}
+
+// Queues ticket `id`'s post-copy work on the unpack stream if no caller has queued it yet, once
+// its copy has landed (the host waits for that). Called without L->mu held. SH_OK also for a
+// ticket that has failed (nothing is left to queue for it).
+int finish_post(sh_loader* L, uint64_t id, const char* who) {
+  hipEvent_t copied = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L->mu);
+    auto it = L->tickets.find(id);
+    if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "%s: unknown ticket %llu", who, (unsigned long long)id);
+    L->issued_cv.wait(lk, [&] { return it->second.state != TicketState::Queued; });
+    if (!it->second.post_pending) return SH_OK;
+    copied = it->second.copied;
+  }
+  const hipError_t e = hipEventSynchronize(copied);
+  if (e != hipSuccess)
+    return sh::fail(SH_ERR_HIP, "%s: waiting for the copy: HIP error %d (%s)", who, (int)e, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(L->mu);
+  auto it = L->tickets.find(id);
+  if (it == L->tickets.end() || !it->second.post_pending) return SH_OK;
+  return launch_post(L, it->second, L->unpack_stream, who);
 }
 
 }  // namespace
@@ -465,6 +516,11 @@ extern "C" int sh_loader_destroy(sh_loader* L) {
   }
   L->advice_cv.notify_all();
   if (L->advisor.joinable()) L->advisor.join();
+  // tickets never waited for still get their post-copy work, as they would have on release
+  std::vector<uint64_t> pending;
+  for (const auto& kv : L->tickets)
+    if (kv.second.post_pending) pending.push_back(kv.first);
+  for (uint64_t id : pending) (void)finish_post(L, id, "sh_loader_destroy");
   (void)hipStreamSynchronize(L->copy_stream);
   (void)hipStreamSynchronize(L->unpack_stream);
   for (auto& kv : L->tickets) give_events(L, kv.second);
@@ -580,6 +636,7 @@ extern "C" int sh_loader_submit(sh_loader* L, const sh_load_request* req, void* 
   t.digest = req->digest;
   t.digest_bytes = req->digest_bytes;
   t.digest_chunk = req->digest_chunk;
+  t.post_pending = t.plan != nullptr || t.digest != nullptr;
   L->queue.push_back(id);
   *ticket = id;
   L->cv.notify_one();
@@ -595,6 +652,13 @@ extern "C" int sh_loader_query(sh_loader* L, uint64_t ticket) {
   Ticket& t = it->second;
   if (t.state == TicketState::Queued) return SH_ERR_NOT_READY;
   if (t.state == TicketState::Failed) return sh::fail(t.status, "sh_loader_query: load failed: %s", t.error.c_str());
+  if (t.post_pending) {
+    // the copy has landed: queue the post-copy work on the unpack stream, with nothing to wait for
+    const hipError_t c = hipEventQuery(t.copied);
+    if (c == hipErrorNotReady) return SH_ERR_NOT_READY;
+    SH_HIP(c);
+    if (int st = launch_post(L, t, L->unpack_stream, "sh_loader_query")) return st;
+  }
   const hipError_t e = hipEventQuery(t.done);
   if (e == hipErrorNotReady) return SH_ERR_NOT_READY;
   SH_HIP(e);
@@ -607,6 +671,7 @@ extern "C" int sh_loader_stream_wait(sh_loader* L, uint64_t ticket, void* stream
   std::unique_lock<std::mutex> lk(L->mu);
   Ticket* t = nullptr;
   if (int st = wait_issued(L, ticket, lk, &t, "sh_loader_stream_wait")) return st;
+  if (t->post_pending) return launch_post(L, *t, (hipStream_t)stream, "sh_loader_stream_wait");
   SH_HIP(hipStreamWaitEvent((hipStream_t)stream, t->done, 0));
   return SH_OK;
 }
@@ -614,6 +679,7 @@ extern "C" int sh_loader_stream_wait(sh_loader* L, uint64_t ticket, void* stream
 extern "C" int sh_loader_sync(sh_loader* L, uint64_t ticket) {
   sh::clear_error();
   if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_sync: loader is NULL");
+  if (int st = finish_post(L, ticket, "sh_loader_sync")) return st;
   hipEvent_t done = nullptr;
   {
     std::unique_lock<std::mutex> lk(L->mu);
@@ -628,6 +694,8 @@ extern "C" int sh_loader_sync(sh_loader* L, uint64_t ticket) {
 extern "C" int sh_loader_release(sh_loader* L, uint64_t ticket) {
   sh::clear_error();
   if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_release: loader is NULL");
+  // a ticket nobody waited for still gets its post-copy work: the destination is written on return
+  const int post = finish_post(L, ticket, "sh_loader_release");
   std::unique_lock<std::mutex> lk(L->mu);
   auto it = L->tickets.find(ticket);
   if (it == L->tickets.end()) return sh::fail(SH_ERR_INVALID, "sh_loader_release: unknown ticket %llu", (unsigned long long)ticket);
@@ -645,7 +713,7 @@ extern "C" int sh_loader_release(sh_loader* L, uint64_t ticket) {
     L->tickets.erase(it);
   }
   if (e != hipSuccess) return sh::fail(SH_ERR_HIP, "sh_loader_release: HIP error %d", (int)e);
-  return SH_OK;
+  return post;
 }
 
 extern "C" int sh_loader_set_timing(sh_loader* L, int enable) {
@@ -660,6 +728,7 @@ extern "C" int sh_loader_ticket_times(sh_loader* L, uint64_t ticket, void* ref_e
   sh::clear_error();
   if (L == nullptr || ref_event == nullptr || out3 == nullptr)
     return sh::fail(SH_ERR_INVALID, "sh_loader_ticket_times: NULL argument");
+  if (int st = finish_post(L, ticket, "sh_loader_ticket_times")) return st;
   hipEvent_t start = nullptr, copied = nullptr, done = nullptr;
   {
     std::unique_lock<std::mutex> lk(L->mu);

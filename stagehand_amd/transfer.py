@@ -9,8 +9,9 @@
 for whole blocks:
 
 * ``submit_block_load`` hands a block's source pieces to the native loader
-  (a worker thread: gather into a pinned slab, H2D on the copy stream, unpack
-  kernel on the unpack stream), returning immediately;
+  (a worker thread: gather into a pinned slab, H2D on the copy stream; the
+  unpack kernel then runs on the stream that first waits for the load, or on
+  the loader's unpack stream when the host waits first), returning immediately;
 * ``wait_device`` makes the caller's current stream wait for a transfer on the
   device, without blocking the host (the reference's ``wait`` blocks the host
   in ``event.synchronize()``, src/stagehand/transfer.py:203; ``wait`` here keeps
@@ -344,7 +345,9 @@ class AsyncTransferEngine:
         return cs.value, us.value
 
     def _loader_unpack_stream(self) -> int:
-        """The loader's unpack stream (hipStream_t value): where chunk digests are taken."""
+        """The loader's unpack stream (hipStream_t value): where save-back chunk comparisons run
+        (a load's own digests run where its post-copy work is queued: the waiting stream, or this
+        one when the host waits)."""
         return self.loader_streams()[1]
 
     def _loader_copy_stream(self) -> torch.cuda.ExternalStream:
