@@ -16,6 +16,12 @@ Printed JSON line (one, from rank 0):
              its output is also compared bit for bit with the device output
   cast       the fp32→bf16 unpack variant of the same shapes
   pcie       pinned hipMemcpyAsync H2D bandwidth (1 GiB x 10)
+
+The process runs with GPU_MAX_HW_QUEUES=8 (--hw-queues; HIP reads it when it
+starts, so it is set before torch is imported): HIP maps every stream of a
+process onto that many hardware queues (4 by default), and the streamed legs
+use the compute stream, the block loader's copy and unpack streams and the
+transfer engine's copy stream on top of whatever streams earlier legs made.
 """
 from __future__ import annotations
 
@@ -1585,7 +1591,16 @@ def main() -> int:
                     help="config 5: StagehandConfig.save_back_backlog_mb (default: the gap between the watermarks)")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
+    ap.add_argument("--hw-queues", type=int, default=8,
+                    help="GPU_MAX_HW_QUEUES for this process, set before HIP starts (0: leave the environment's)")
     args = ap.parse_args()
+    if args.hw_queues:
+        if not 1 <= args.hw_queues <= 32:
+            ap.error("--hw-queues must be between 1 and 32")
+        if "torch" in sys.modules:
+            print("bench.py: torch was imported before --hw-queues could take effect", file=sys.stderr)
+            return 2
+        os.environ["GPU_MAX_HW_QUEUES"] = str(args.hw_queues)
 
     if args.trace_summary:
         print(json.dumps(trace_summary(Path(args.trace_summary), args.trace_bytes, args.pcie_gbps)), flush=True)
@@ -1668,6 +1683,7 @@ def main() -> int:
             "rows": sum(g.rows for g in regions),
             "algo_bytes_per_step": algo,
             "parallelism": "single GPU",
+            "hip_hw_queues": os.environ.get("GPU_MAX_HW_QUEUES"),
         },
         "roofline": {
             "kernel": "sh_dequant_i8_bf16_kernel",
