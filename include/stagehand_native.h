@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SH_ABI_VERSION 7
+#define SH_ABI_VERSION 8
 
 enum sh_status {
   SH_OK = 0,
@@ -422,6 +422,15 @@ int sh_loader_query(sh_loader* loader, uint64_t ticket);
 int sh_loader_stream_wait(sh_loader* loader, uint64_t ticket, void* stream);
 /* Host waits until the destination is written. */
 int sh_loader_sync(sh_loader* loader, uint64_t ticket);
+/* The copy alone (no reference counterpart; the reference's transfer is its
+ * copy, src/stagehand/transfer.py:126-143, which the in-flight bound of
+ * transfer.py:258-276 counts): SH_OK once the ticket's host-to-device copies
+ * have landed, whether or not its post-copy work has run, SH_ERR_NOT_READY
+ * before; and a host wait for that point. The post-copy work of a ticket that
+ * sh_loader_stream_wait queued on a compute stream completes only when that
+ * stream reaches it, so a bound on copies in flight waits on these. */
+int sh_loader_query_copy(sh_loader* loader, uint64_t ticket);
+int sh_loader_sync_copy(sh_loader* loader, uint64_t ticket);
 /* Forgets a ticket (waits for its device work first, post-copy work included:
  * the destination and digests are written on return). */
 int sh_loader_release(sh_loader* loader, uint64_t ticket);

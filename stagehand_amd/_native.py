@@ -162,6 +162,8 @@ _SIGNATURES: dict[str, list] = {
     "sh_loader_query": [_vp, ctypes.c_uint64],
     "sh_loader_stream_wait": [_vp, ctypes.c_uint64, _vp],
     "sh_loader_sync": [_vp, ctypes.c_uint64],
+    "sh_loader_query_copy": [_vp, ctypes.c_uint64],
+    "sh_loader_sync_copy": [_vp, ctypes.c_uint64],
     "sh_loader_release": [_vp, ctypes.c_uint64],
     "sh_loader_set_timing": [_vp, _i32],
     "sh_loader_ticket_times": [_vp, ctypes.c_uint64, _vp, _vp],
@@ -261,7 +263,7 @@ TURBO_SPAN_DTYPE = np.dtype([("block", "<u4"), ("kind", "<u4"), ("start_ns", "<u
                              ("bytes", "<u8")])
 TURBO_SPAN_WRITEBACK, TURBO_SPAN_HOST_WAIT = 0, 1
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

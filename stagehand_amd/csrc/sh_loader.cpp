@@ -665,6 +665,36 @@ extern "C" int sh_loader_query(sh_loader* L, uint64_t ticket) {
   return SH_OK;
 }
 
+extern "C" int sh_loader_query_copy(sh_loader* L, uint64_t ticket) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_query_copy: loader is NULL");
+  std::lock_guard<std::mutex> lk(L->mu);
+  auto it = L->tickets.find(ticket);
+  if (it == L->tickets.end())
+    return sh::fail(SH_ERR_INVALID, "sh_loader_query_copy: unknown ticket %llu", (unsigned long long)ticket);
+  Ticket& t = it->second;
+  if (t.state == TicketState::Queued) return SH_ERR_NOT_READY;
+  if (t.state == TicketState::Failed) return sh::fail(t.status, "sh_loader_query_copy: load failed: %s", t.error.c_str());
+  const hipError_t e = hipEventQuery(t.copied);
+  if (e == hipErrorNotReady) return SH_ERR_NOT_READY;
+  SH_HIP(e);
+  return SH_OK;
+}
+
+extern "C" int sh_loader_sync_copy(sh_loader* L, uint64_t ticket) {
+  sh::clear_error();
+  if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_sync_copy: loader is NULL");
+  hipEvent_t copied = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L->mu);
+    Ticket* t = nullptr;
+    if (int st = wait_issued(L, ticket, lk, &t, "sh_loader_sync_copy")) return st;
+    copied = t->copied;
+  }
+  SH_HIP(hipEventSynchronize(copied));
+  return SH_OK;
+}
+
 extern "C" int sh_loader_stream_wait(sh_loader* L, uint64_t ticket, void* stream) {
   sh::clear_error();
   if (L == nullptr) return sh::fail(SH_ERR_INVALID, "sh_loader_stream_wait: loader is NULL");

@@ -231,6 +231,7 @@ class TransferHandle:
     keepalive: list = field(default_factory=list, repr=False)
     device_waited: bool = False
     host_clock: bool = False  # submitted_at is on time.perf_counter (set while a trace runs)
+    copy_landed: bool = False  # a block load's copies have landed (its unpack / digests may not have run)
 
 
 @dataclass
@@ -1017,11 +1018,26 @@ class AsyncTransferEngine:
             self._next_handle_id += 1
         return TransferHandle(hid, block_id, direction, None, time.monotonic(), size_bytes)
 
+    def _copy_outstanding(self, handle: TransferHandle) -> bool:
+        """Whether ``handle``'s copy is still in flight. For a block load that is its H2D
+        copies alone: its unpack and digests run where its first waiter queued them, possibly far
+        ahead on a compute stream, and are not a transfer. A failed load holds no copy; its
+        failure is raised where it is waited for. Called with the engine's lock held."""
+        if handle.completed or handle.copy_landed:
+            return False
+        if handle.ticket is not None:
+            st = _native.lib().sh_loader_query_copy(self._loader, handle.ticket)
+            if st == _native.SH_ERR_NOT_READY:
+                return True
+            handle.copy_landed = True
+            return False
+        return True
+
     def _wait_for_slot(self) -> None:
-        """Backpressure: block while ``max_inflight`` transfers are outstanding.
+        """Backpressure: block while ``max_inflight`` copies are outstanding.
 
         The reference polls in 1 ms condition waits (src/stagehand/transfer.py:258-276);
-        here the host sleeps in a native wait on the oldest transfer (copies on one
+        here the host sleeps in a native wait on the oldest outstanding copy (copies on one
         stream complete in order), so a freed slot is seen at once. A wait above
         1 ms is logged at debug level: in a PCIe-bound stream it is the normal pacing.
         """
@@ -1030,14 +1046,16 @@ class AsyncTransferEngine:
         while True:
             with self._cond:
                 self._reap_completed_locked()
-                if len(self._inflight) < self._max_inflight:
+                outstanding = [h for h in self._inflight if self._copy_outstanding(h)]
+                if len(outstanding) < self._max_inflight:
                     break
-                oldest = self._inflight[0]
+                oldest = outstanding[0]
             with self.host_wait("inflight_slot"):
                 if oldest.ticket is not None:
-                    st = _native.lib().sh_loader_sync(self._loader, oldest.ticket)
+                    st = _native.lib().sh_loader_sync_copy(self._loader, oldest.ticket)
                     if st != _native.SH_OK:
                         self._raise_transfer(st, oldest.block_id, oldest.direction)
+                    oldest.copy_landed = True
                 elif oldest.event is not None:
                     oldest.event.synchronize()
                 else:

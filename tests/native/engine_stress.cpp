@@ -99,6 +99,20 @@ void finish_load(sh_loader* L, sh_saveback* sb, hipStream_t s, Load& ld, Rng& r)
   // a load's unpack and digests are queued by whichever of these comes first; a release with no
   // wait before it still leaves the destination and the digests written
   bool released = false;
+  // the copy alone first, now and then (the in-flight bound waits on it)
+  switch (r.below(3)) {
+    case 0:
+      check(sh_loader_sync_copy(L, ld.ticket) == SH_OK, "sh_loader_sync_copy", ld.kind);
+      break;
+    case 1: {
+      int st;
+      while ((st = sh_loader_query_copy(L, ld.ticket)) == SH_ERR_NOT_READY) std::this_thread::yield();
+      check(st == SH_OK, "sh_loader_query_copy", ld.kind);
+      break;
+    }
+    default:
+      break;
+  }
   switch (r.below(4)) {
     case 0: {
       int st;

@@ -132,27 +132,31 @@ struct FakeStream {
 };
 
 std::mutex g_streams_mu;
-std::set<FakeStream*>* g_streams = nullptr;  // every live stream, the null stream included
+// every live stream, the null stream included; the map owns them, and drain_all holds a reference
+// to each stream it drains, so a stream destroyed meanwhile is deleted once that drain ends
+std::map<FakeStream*, std::shared_ptr<FakeStream>>* g_streams = nullptr;
 FakeStream* g_null = nullptr;
 
 FakeStream* stream_of(hipStream_t s) {
   if (s != nullptr) return reinterpret_cast<FakeStream*>(s);
   std::lock_guard<std::mutex> lk(g_streams_mu);
   if (g_null == nullptr) {
-    g_null = new FakeStream();
-    if (g_streams == nullptr) g_streams = new std::set<FakeStream*>();
-    g_streams->insert(g_null);
+    auto sp = std::make_shared<FakeStream>();
+    g_null = sp.get();
+    if (g_streams == nullptr) g_streams = new std::map<FakeStream*, std::shared_ptr<FakeStream>>();
+    (*g_streams)[g_null] = std::move(sp);
   }
   return g_null;
 }
 
 void drain_all() {
-  std::vector<FakeStream*> all;
+  std::vector<std::shared_ptr<FakeStream>> all;
   {
     std::lock_guard<std::mutex> lk(g_streams_mu);
-    if (g_streams != nullptr) all.assign(g_streams->begin(), g_streams->end());
+    if (g_streams != nullptr)
+      for (const auto& kv : *g_streams) all.push_back(kv.second);
   }
-  for (FakeStream* s : all) s->drain();
+  for (const auto& s : all) s->drain();
 }
 
 void complete(const std::shared_ptr<EventState>& st, uint64_t gen) {
@@ -298,11 +302,12 @@ hipError_t hipMemcpyAsync(void* dst, const void* src, size_t n, hipMemcpyKind, h
 // ── streams and events ────────────────────────────────────────────────────
 
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned int) {
-  FakeStream* fs = new FakeStream();
+  auto sp = std::make_shared<FakeStream>();
+  FakeStream* fs = sp.get();
   {
     std::lock_guard<std::mutex> lk(g_streams_mu);
-    if (g_streams == nullptr) g_streams = new std::set<FakeStream*>();
-    g_streams->insert(fs);
+    if (g_streams == nullptr) g_streams = new std::map<FakeStream*, std::shared_ptr<FakeStream>>();
+    (*g_streams)[fs] = std::move(sp);
   }
   *s = reinterpret_cast<hipStream_t>(fs);
   return hipSuccess;
@@ -310,11 +315,15 @@ hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned int) {
 hipError_t hipStreamDestroy(hipStream_t s) {
   if (s == nullptr) return hipErrorInvalidHandle;
   FakeStream* fs = reinterpret_cast<FakeStream*>(s);
+  std::shared_ptr<FakeStream> sp;
   {
     std::lock_guard<std::mutex> lk(g_streams_mu);
-    g_streams->erase(fs);
+    auto it = g_streams->find(fs);
+    if (it == g_streams->end()) return hipErrorInvalidHandle;
+    sp = std::move(it->second);
+    g_streams->erase(it);
   }
-  delete fs;  // runs what is queued, then joins
+  sp.reset();  // the last reference runs what is queued, then joins
   return hipSuccess;
 }
 hipError_t hipStreamSynchronize(hipStream_t s) {
