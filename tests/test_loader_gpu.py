@@ -82,3 +82,41 @@ def test_post_copy_work_runs_on_every_consumption_path(how):
     finally:
         eng.shutdown()
         pool.shutdown()
+
+
+def test_inflight_bound_counts_copies_not_post_copy_work():
+    """The in-flight bound (the reference's max_inflight, src/stagehand/transfer.py:258-276) limits
+    copies: a load whose unpack waits on a busy stream, behind work the host queued ahead, holds
+    no slot once its copy has landed, and the next submit does not wait for that stream."""
+    from test_streaming_gpu import _sleep_cycles_for
+
+    pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
+    eng = AsyncTransferEngine(pool, max_inflight=1)
+    busy = torch.cuda.Stream()
+    cycles = _sleep_cycles_for(400.0)
+    try:
+        src, s_off, plan, want = _block(7)
+        dst = torch.empty(2 * want.size, dtype=torch.uint8, device="cuda")
+        source = BlockSource([(0, torch.from_numpy(src))], src.size, plan=plan, scale_off=s_off, n_scale=ROWS)
+        h1 = eng.submit_block_load("first", source, dst)
+        with torch.cuda.stream(busy):
+            torch.cuda._sleep(cycles)  # about 400 ms of device work queued ahead
+            eng.wait_device(h1)        # the unpack goes behind it
+        while eng._copy_outstanding(h1):
+            pass
+        src2, s_off2, plan2, want2 = _block(8)
+        dst2 = torch.empty(2 * want2.size, dtype=torch.uint8, device="cuda")
+        eng.host_wait_ms.clear()
+        h2 = eng.submit_block_load("second", BlockSource([(0, torch.from_numpy(src2))], src2.size, plan=plan2,
+                                                         scale_off=s_off2, n_scale=ROWS), dst2)
+        assert eng.host_wait_ms.get("inflight_slot", 0.0) < 100.0, eng.host_wait_ms
+        assert not busy.query(), "the busy stream finished before the second submit: the test proves nothing"
+        eng.wait(h2)
+        busy.synchronize()
+        eng.wait(h1)
+        np.testing.assert_array_equal(dst.cpu().numpy().view(np.uint16), want)
+        np.testing.assert_array_equal(dst2.cpu().numpy().view(np.uint16), want2)
+    finally:
+        busy.synchronize()
+        eng.shutdown()
+        pool.shutdown()
