@@ -47,6 +47,27 @@ def _first_tensor(output: object) -> torch.Tensor | None:
     return None
 
 
+def _hint_hw_queues() -> None:
+    """Logs once when HIP runs with fewer than 8 hardware queues (GPU_MAX_HW_QUEUES, 4 by default).
+    HIP maps every stream onto those queues, and streams that share one run in the order their
+    work was queued: the save-backs' chunk comparisons, on the block loader's unpack stream, then
+    run behind compute queued after them, and training steps wait longer on save-backs."""
+    global _HW_QUEUES_HINTED
+    if _HW_QUEUES_HINTED:
+        return
+    _HW_QUEUES_HINTED = True
+    try:
+        queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+    except ValueError:
+        return
+    if queues < 8:
+        log.info("StagehandRuntime: HIP has %d hardware queues (GPU_MAX_HW_QUEUES); training with changed-chunk "
+                 "save-backs runs faster with 8, set before HIP starts", queues)
+
+
+_HW_QUEUES_HINTED = False
+
+
 class StagehandRuntime:
     def __init__(
         self,
@@ -78,6 +99,8 @@ class StagehandRuntime:
         self._engine = AsyncTransferEngine(pool=self._pool, max_inflight=config.max_inflight_transfers,
                                            pin_sources=config.pinned_source_cache,
                                            save_back=config.save_back_engine)
+        if not inference_mode and config.save_back_changed_chunks and torch.cuda.is_available():
+            _hint_hw_queues()
         self._scheduler = StagehandScheduler(
             registry=self._registry, residency=self._residency, transfer_engine=self._engine, budget=self._budget,
             policy=StaticLookaheadPolicy(prefetch_window=config.prefetch_window_blocks,

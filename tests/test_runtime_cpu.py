@@ -60,3 +60,20 @@ def test_checkpointed_training_releases_every_reference(checkpoint):
             # three accumulated backward passes against one
             assert torch.allclose(p.grad.float(), 3 * q.grad.float(), rtol=2e-2, atol=1e-4), n
     rt.shutdown()
+
+
+def test_hardware_queue_hint_logs_once_below_eight(monkeypatch, caplog):
+    """Training with changed-chunk save-backs logs one hint when HIP has fewer than 8 hardware
+    queues, and none with 8."""
+    import logging
+
+    from stagehand_amd import runtime as rt_mod
+
+    for queues, expect in (("4", 1), ("8", 0)):
+        monkeypatch.setattr(rt_mod, "_HW_QUEUES_HINTED", False)
+        monkeypatch.setenv("GPU_MAX_HW_QUEUES", queues)
+        caplog.clear()
+        with caplog.at_level(logging.INFO, logger="stagehand_amd.runtime"):
+            rt_mod._hint_hw_queues()
+            rt_mod._hint_hw_queues()
+        assert sum("hardware queues" in r.getMessage() for r in caplog.records) == expect, queues
