@@ -87,30 +87,51 @@ def test_post_copy_work_runs_on_every_consumption_path(how):
 def test_inflight_bound_counts_copies_not_post_copy_work():
     """The in-flight bound (the reference's max_inflight, src/stagehand/transfer.py:258-276) limits
     copies: a load whose unpack waits on a busy stream, behind work the host queued ahead, holds
-    no slot once its copy has landed, and the next submit does not wait for that stream."""
+    no slot once its copy has landed, and the next submit does not wait for that stream.
+
+    Everything that may synchronise the device (plan creation copies its tables with hipMemcpy;
+    freeing device memory, as the garbage collection of an earlier test's plan would, waits for
+    the whole device) happens before the busy stream's spin is queued, with the collector paused."""
+    import gc
+
     from test_streaming_gpu import _sleep_cycles_for
 
     pool = PinnedPool(total_mb=4, slab_mb=1, alignment=512)
     eng = AsyncTransferEngine(pool, max_inflight=1)
     busy = torch.cuda.Stream()
     cycles = _sleep_cycles_for(400.0)
+    src, s_off, plan, want = _block(7)
+    src2, s_off2, plan2, want2 = _block(8)
+    dst = torch.empty(2 * want.size, dtype=torch.uint8, device="cuda")
+    dst2 = torch.empty(2 * want2.size, dtype=torch.uint8, device="cuda")
+    # two staging buffers of the loads' size in the allocator's cache, so the submits allocate nothing
+    warm = [torch.empty(max(src.size, src2.size), dtype=torch.uint8, device="cuda") for _ in range(2)]
+    del warm
+    source = BlockSource([(0, torch.from_numpy(src))], src.size, plan=plan, scale_off=s_off, n_scale=ROWS)
+    source2 = BlockSource([(0, torch.from_numpy(src2))], src2.size, plan=plan2, scale_off=s_off2, n_scale=ROWS)
+    # one load through the same path first: the loader, its streams and the kernels are set up
+    hw = eng.submit_block_load("warm-up", source, dst)
+    eng.wait_device(hw)
+    eng.wait(hw)
+    gc.collect()
+    torch.cuda.synchronize()
+    gc.disable()
     try:
-        src, s_off, plan, want = _block(7)
-        dst = torch.empty(2 * want.size, dtype=torch.uint8, device="cuda")
-        source = BlockSource([(0, torch.from_numpy(src))], src.size, plan=plan, scale_off=s_off, n_scale=ROWS)
         h1 = eng.submit_block_load("first", source, dst)
         with torch.cuda.stream(busy):
             torch.cuda._sleep(cycles)  # about 400 ms of device work queued ahead
             eng.wait_device(h1)        # the unpack goes behind it
         while eng._copy_outstanding(h1):
             pass
-        src2, s_off2, plan2, want2 = _block(8)
-        dst2 = torch.empty(2 * want2.size, dtype=torch.uint8, device="cuda")
         eng.host_wait_ms.clear()
-        h2 = eng.submit_block_load("second", BlockSource([(0, torch.from_numpy(src2))], src2.size, plan=plan2,
-                                                         scale_off=s_off2, n_scale=ROWS), dst2)
-        assert eng.host_wait_ms.get("inflight_slot", 0.0) < 100.0, eng.host_wait_ms
-        assert not busy.query(), "the busy stream finished before the second submit: the test proves nothing"
+        h2 = eng.submit_block_load("second", source2, dst2)
+        waited = eng.host_wait_ms.get("inflight_slot", 0.0)
+        still_busy = not busy.query()
+    finally:
+        gc.enable()
+    try:
+        assert still_busy, "the busy stream finished before the second submit: the test proves nothing"
+        assert waited < 100.0, eng.host_wait_ms
         eng.wait(h2)
         busy.synchronize()
         eng.wait(h1)
